@@ -1,0 +1,232 @@
+/*
+ * r4q.h — C ABI of the MI355X (gfx950) decode-step library `librdna4q.so`.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * handle passed as `void*` (NULL = the legacy default stream), and returns an
+ * int status: R4Q_OK (0) or a negative R4Q_E* code.  The text of the last
+ * failure on the calling thread is available from r4q_last_error().  No C++
+ * exception crosses this boundary and no entry point takes a torch type.
+ *
+ * Tensor conventions (all row-major, contiguous):
+ *   fp16 values are IEEE binary16 carried as uint16_t bit patterns.
+ *   INT4 weight  w  [N, K/2]  uint8, byte = q[2j] | q[2j+1] << 4, q in 0..15
+ *   INT8 weight  w  [N, K]    uint8, q in 0..255 (symmetric int8 checkpoints:
+ *                              q = int8 + 128 with zero-point 128)
+ *   FP16 weight  w  [N, K]    fp16
+ *   scale/zero  sz  [N, K/32, 2] fp16, interleaved (scale, zero-point) per
+ *                              32-element block; unused for FP16 weights.
+ *   dequantised weight = fp16( (float(q) - float(zp)) * float(scale) )
+ *   FP8 KV cache [B, Hk, max_seq, head_dim] uint8, E4M3 codes written by the
+ *   reference recipe (see r4q_fp16_to_fp8), optional per-head fp32 scale:
+ *   stored = fp8(value * (1/scale)), read back as fp8_value * scale.
+ *
+ * `wbits` selects the weight format: 4 (INT4 asym), 8 (INT8 asym), 16 (FP16).
+ *
+ * Reference interfaces replaced (JohnTDI-cpu/rdna4-quant,
+ * hip_int4/int4_decode_step.hip, pybind table at :3620-3636):
+ *   r4q_dequant_int4     <- dequant_int4            (:3590-3603)
+ *   r4q_fp16_to_fp8      <- fp16_to_fp8             (:3611-3618)
+ *   r4q_gemv             <- dbg_gemv / launch_gemv  (:3541-3550, :230-235)
+ *   r4q_gemm             <- dbg_gemm / dequant_matmul_out (:3552-3561, :1973-1988)
+ *   r4q_rmsnorm          <- dbg_rmsnorm             (:3473-3484)
+ *   r4q_res_rmsnorm      <- dbg_fused_res_norm      (:3524-3539)
+ *   r4q_rmsnorm_fwht     <- fused_rmsnorm_fwht      (:1195-1237)
+ *   r4q_res_rmsnorm_fwht <- fused_res_norm_fwht     (:1143-1192)
+ *   r4q_fwht32           <- hadamard_rotate_batched (:766-786)
+ *   r4q_silu_mul_fwht    <- silu_hadamard_ds        (:1031-1051)
+ *   r4q_silu_mul         <- silu_mul_batched        (:2112-2122)
+ *   r4q_head_rmsnorm     <- dbg_head_rmsnorm        (:3486-3504)
+ *   r4q_rope             <- dbg_rope                (:3506-3522)
+ *   r4q_head_norm_rope_kv<- head_rmsnorm_rope_kv    (:1620-1683)
+ *   r4q_flash_decode     <- launch_flash_decode     (:1547-1593)
+ *   r4q_decode_step      <- decode_step / decode_step_logits (:2343-2595)
+ *   r4q_decode_bench     <- decode_bench / decode_bench_graph (:2601-3041)
+ *   r4q_decode_profile   <- decode_profile          (:3047-3273)
+ *   r4q_decode_loop      <- decode_loop             (:3284-3466)
+ *   r4q_prefill_logits   <- prefill_logits          (:2127-2320)
+ */
+#ifndef R4Q_H
+#define R4Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Only the entry points below are exported from librdna4q.so. */
+#if defined(__GNUC__)
+#define R4Q_API __attribute__((visibility("default")))
+#else
+#define R4Q_API
+#endif
+
+#define R4Q_OK            0
+#define R4Q_EINVAL       -1   /* bad pointer, size, shape or format */
+#define R4Q_EUNSUPPORTED -2   /* valid request this build does not implement */
+#define R4Q_EHIP         -3   /* a HIP runtime call failed */
+#define R4Q_ENOMEM       -4   /* device allocation failed */
+
+/* Text of the last error on this thread ("" if none). */
+R4Q_API const char* r4q_last_error(void);
+/* ABI version: bumped when a signature or struct layout changes. */
+R4Q_API int r4q_abi_version(void);
+
+/* ---------------------------------------------------------------- codecs */
+
+/* out[N,K] fp16 = dequant(packed INT4 [N,K/2], sz [N,K/32,2]).  K % 32 == 0. */
+R4Q_API int r4q_dequant_int4(const void* packed, const void* sz, void* out,
+                     int64_t N, int64_t K, void* stream);
+/* out[N,K] fp16 = dequant(INT8 q [N,K], sz [N,K/32,2]).  K % 32 == 0. */
+R4Q_API int r4q_dequant_int8(const void* q, const void* sz, void* out,
+                     int64_t N, int64_t K, void* stream);
+/* dst[n] uint8 = E4M3 code of src[n] (fp16) by the reference recipe
+ * (hip:47-68): clamp to +-448 (NaN -> 448), exponent rebias, keep 3 mantissa
+ * bits rounding up when fp32 mantissa bit 19 is set, |x| < 2^-6 -> +-0,
+ * exponent >= 15 -> +-0x7E (448).  No scaling. */
+R4Q_API int r4q_fp16_to_fp8(const void* src, void* dst, int64_t n, void* stream);
+/* dst[n] fp16 = value of E4M3 code src[n] (exact for every emitted code). */
+R4Q_API int r4q_fp8_to_fp16(const void* src, void* dst, int64_t n, void* stream);
+
+/* ---------------------------------------------------------------- linear */
+
+/* y[N] fp16 = W x with W given by (w, sz, wbits), x[K] fp16, fp32 accumulate.
+ * K % 32 == 0, N >= 1. */
+R4Q_API int r4q_gemv(const void* x, const void* w, const void* sz, void* y,
+             int64_t N, int64_t K, int wbits, void* stream);
+/* y[M,N] fp16 = x[M,K] W^T (same weight formats), fp32 accumulate.
+ * Small M streams the weights once for all rows; large M dequantises tiles
+ * on the fly into an MFMA GEMM. */
+R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
+             int64_t M, int64_t N, int64_t K, int wbits, void* stream);
+
+/* ------------------------------------------------------ norms / rotations */
+
+/* y = fp16(x * rrms * w), rrms = 1/sqrt(mean(x^2) + eps), per row of D. */
+R4Q_API int r4q_rmsnorm(const void* x, const void* w, void* y,
+                int64_t rows, int64_t D, float eps, void* stream);
+/* r = fp16(x + res) -> res_out; y = fp16(float(r) * rrms * w) with rrms from
+ * the fp32 sum (x + res). */
+R4Q_API int r4q_res_rmsnorm(const void* x, const void* res, const void* w, void* y,
+                    void* res_out, int64_t rows, int64_t D, float eps,
+                    void* stream);
+/* y = fp16(H32 (x * rrms * w) / sqrt(32)) per 32-element chunk (D % 32 == 0). */
+R4Q_API int r4q_rmsnorm_fwht(const void* x, const void* w, void* y,
+                     int64_t rows, int64_t D, float eps, void* stream);
+/* residual + RMSNorm + FWHT-32 in one pass: res_out = fp16(a + b);
+ * y = FWHT32(float(res_out) * rrms * w) with rrms from the fp32 sum. */
+R4Q_API int r4q_res_rmsnorm_fwht(const void* a, const void* b, const void* w,
+                         void* y, void* res_out, int64_t rows, int64_t D,
+                         float eps, void* stream);
+/* y = fp16(H32 x / sqrt(32)) per 32-element chunk of n elements (n % 32 == 0). */
+R4Q_API int r4q_fwht32(const void* x, void* y, int64_t n, void* stream);
+/* y[r, i] = fp16(FWHT32(silu(g[r,i]) * u[r,i])), i < I; g/u row stride
+ * `in_stride`, y row stride `out_stride` (elements).  y may alias g. */
+R4Q_API int r4q_silu_mul_fwht(const void* g, const void* u, void* y, int64_t rows,
+                      int64_t I, int64_t in_stride, int64_t out_stride,
+                      void* stream);
+/* y[r, i] = fp16(silu(g[r,i]) * u[r,i]) (no rotation). */
+R4Q_API int r4q_silu_mul(const void* g, const void* u, void* y, int64_t rows,
+                 int64_t I, int64_t in_stride, int64_t out_stride,
+                 void* stream);
+
+/* ---------------------------------------------------------- attention I/O */
+
+/* Per-head RMSNorm of q [H, D] and k [Hk, D] into q_out / k_out (fp16). */
+R4Q_API int r4q_head_rmsnorm(const void* q, const void* k, const void* qw,
+                     const void* kw, void* q_out, void* k_out, int64_t H,
+                     int64_t Hk, int64_t D, float eps, void* stream);
+/* Half-split RoPE at position `pos` (tables cos/sin [P, D/2] fp16). */
+R4Q_API int r4q_rope(const void* q, const void* k, const void* cos_t,
+             const void* sin_t, void* q_out, void* k_out, int64_t H,
+             int64_t Hk, int64_t D, int64_t pos, void* stream);
+/* Decode-step QK-norm + RoPE + FP8 KV write for B sequences at one position.
+ * q/k/v: row b at qkv + b*qkv_stride (q [H,D] | k [Hk,D] | v [Hk,D]).
+ * q_out/k_out (fp16, may alias q/k) get the normed+rotated vectors; the K and
+ * V caches [B, Hk, max_seq, D] get FP8 codes at `pos`.  k_scale / v_scale are
+ * [Hk] fp32 or NULL (scale 1).  Requires D == 128. */
+R4Q_API int r4q_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw,
+                          const void* kw, void* q_out, int64_t q_out_stride,
+                          void* k_cache, void* v_cache, const float* k_scale,
+                          const float* v_scale, const void* cos_t,
+                          const void* sin_t, int64_t B, int64_t H, int64_t Hk,
+                          int64_t D, float eps, int64_t max_seq, int64_t pos,
+                          void* stream);
+
+/* --------------------------------------------------------------- context */
+
+typedef struct r4q_ctx r4q_ctx;
+/* A context owns device scratch (attention partials, decode-step buffers,
+ * captured graphs) for one device.  Not thread-safe; use one per stream. */
+R4Q_API int r4q_ctx_create(r4q_ctx** out);
+R4Q_API int r4q_ctx_destroy(r4q_ctx* ctx);
+
+/* Split-K flash-decode over an FP8 KV cache for B sequences at seq_len
+ * positions: out[b, h*D + d] = softmax(q k^T / sqrt(D)) v for query head h
+ * and KV head h / (H/Hk).  q row b at q + b*q_stride.  When `fwht` != 0 the
+ * output gets the FWHT-32 rotation (the O-projection input).  Requires
+ * D == 128, H % Hk == 0. */
+R4Q_API int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
+                     const void* k_cache, const void* v_cache,
+                     const float* k_scale, const float* v_scale, void* out,
+                     int64_t B, int64_t H, int64_t Hk, int64_t D,
+                     int64_t max_seq, int64_t seq_len, int fwht, void* stream);
+
+/* ----------------------------------------------------------- decode model */
+
+/* One decoder layer's tensors.  *_bits is 4, 8 or 16 per matrix.
+ * qkv = cat(q, k, v) rows; gate_up = cat(gate, up) rows. */
+typedef struct r4q_layer {
+  const void* qkv_w;  const void* qkv_s;  int64_t qkv_N;  int32_t qkv_bits;
+  const void* o_w;    const void* o_s;    int64_t o_N;    int32_t o_bits;
+  const void* gu_w;   const void* gu_s;   int64_t gu_N;   int32_t gu_bits;
+  const void* down_w; const void* down_s; int64_t down_N; int32_t down_bits;
+  const void* in_norm; const void* post_norm; const void* q_norm;
+  const void* k_norm;
+  void* k_cache; void* v_cache;              /* [B, Hk, max_seq, D] uint8 */
+  const float* k_scale; const float* v_scale;/* [Hk] fp32 or NULL        */
+} r4q_layer;
+
+typedef struct r4q_model {
+  int32_t n_layers, n_heads, n_kv_heads, head_dim, hidden, inter;
+  float eps;
+  int32_t max_seq;         /* KV cache capacity (positions)            */
+  int32_t rope_len;        /* rows of the RoPE tables                  */
+  const r4q_layer* layers; /* n_layers entries                         */
+  const void* rope_cos; const void* rope_sin; /* [rope_len, D/2] fp16   */
+  const void* final_norm;  /* [hidden] fp16 (NULL: no LM head)         */
+  const void* lm_w; const void* lm_s; int64_t lm_N, lm_K; int32_t lm_bits;
+  const void* embed;       /* [vocab, hidden] fp16 or NULL             */
+  int64_t vocab;
+} r4q_model;
+
+/* One decode step for B sequences at position `pos` (same for all rows).
+ * hidden_in [B, hidden] fp16.  Writes hidden_out [B, hidden] (may be NULL)
+ * and, when logits != NULL and the model has an LM head, logits [B, lm_N]
+ * fp16.  KV caches are written at `pos`; positions < pos must be filled. */
+R4Q_API int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                    int64_t B, int64_t pos, void* hidden_out, void* logits,
+                    void* stream);
+/* Run `num_tokens` steps from start_pos.  use_graph != 0 captures one step
+ * into a hipGraph and replays it with the position held in device memory.
+ * Greedy next token (argmax + embedding gather) runs on the device between
+ * steps when the model has an embedding; token ids (int64 [num_tokens, B])
+ * are written to `tokens_out` when it is not NULL.  B sequences. */
+R4Q_API int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                     int64_t B, int64_t num_tokens, int64_t start_pos,
+                     int use_graph, void* tokens_out, void* stream);
+/* Time one step by kernel category with HIP events:
+ * out_ms[5] = {total, gemv, attention, norm, rest}. */
+R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                       int64_t pos, float* out_ms, void* stream);
+
+/* Prefill M tokens from position 0: embedding of ids (int64 [M]) through all
+ * layers; writes logits [M, lm_N] fp16 (NULL: skip the LM head) and, when
+ * write_kv != 0, the FP8 KV caches at positions 0..M-1. */
+R4Q_API int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* ids,
+                       int64_t M, void* logits, int write_kv, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* R4Q_H */

@@ -1,0 +1,327 @@
+// Split-K flash-decode over the FP8 E4M3 KV cache (GQA), with the log-sum-exp
+// merge and the optional FWHT-32 output rotation in a second pass.
+//
+// Replaces the reference's launch_flash_decode (hip:1547-1593) with its
+// flash_decode_partial (hip:1326-1412), flash_decode_reduce (hip:1416-1463)
+// and flash_decode_fused (hip:1471-1542); softmax semantics follow SDPA
+// (int4_engine_v5.py:245).  Unlike the reference, Q stays fp16 (the
+// reference's FP8 quantisation of Q costs ~2.7e-2 rel-L2 and its
+// dot4_f32_fp8_fp8 instruction does not exist on gfx950), and K/V carry an
+// optional per-head fp32 scale.
+//
+// Partial pass, one workgroup (4 waves) per (split, kv head, sequence):
+//  * QK: 4 lanes per position, each owning 32 head dims; the position's 32 K
+//    bytes arrive in two 128-bit loads and are widened to fp16 by placing the
+//    E4M3 fields into fp16 fields (exact, value / 256); the GQA group's query
+//    heads live in registers as fp16 pairs so every K byte feeds all of them
+//    through v_dot2_f32_f16; the 4 partial dots are combined with DPP.
+//  * scores -> LDS; per-head max, exp and the fp16-rounded probabilities
+//    (pairs of positions) -> LDS.
+//  * PV: each lane owns 4 head dims; two positions' V bytes are interleaved
+//    with v_perm so v_dot2 contracts over the position pair; partials are
+//    reduced across half-waves and waves through LDS.
+// Combine pass: m* = max_s m_s; out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s,
+// then FWHT-32 in registers (4 lanes x 32 dims per head).
+#include <math.h>
+
+#include "r4q_ctx.hpp"
+#include "r4q_device.hpp"
+#include "r4q_host.hpp"
+
+namespace r4q {
+namespace {
+
+constexpr int kMaxSplitLen = 256;
+constexpr int kPart = 130;  // floats per (seq, head, split): m, l, o[128]
+
+// Four E4M3 bytes (b0 b1 b2 b3) -> fp16 pairs (b0, b2) and (b1, b3), each
+// value divided by 256 (exact).
+__device__ __forceinline__ void fp8x4_to_h2_div256(uint32_t w, uint32_t& h02, uint32_t& h13) {
+  uint32_t m1 = 0x80008000u, m2 = 0x3F803F80u;
+  asm volatile("" : "+v"(m1), "+v"(m2));
+  h02 = ((w << 8) & m1) | ((w << 7) & m2);
+  h13 = (w & m1) | ((w >> 1) & m2);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_partial_kernel(
+    const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
+    const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
+    float* __restrict__ part, int H, int Hk, int max_seq, int L_host,
+    const int* __restrict__ L_dev, int nsplit) {
+  const int sp = blockIdx.x, kh = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int L = L_dev ? *L_dev : L_host;
+  const int S = (L + nsplit - 1) / nsplit;
+  const int s0 = sp * S;
+  const int n = max(0, min(L, s0 + S) - s0);  // <= kMaxSplitLen
+
+  // 128-bit LDS accesses below need 16-byte aligned rows
+  __shared__ __align__(16) float sc[G][kMaxSplitLen];
+  __shared__ __align__(16) uint32_t pp[G][kMaxSplitLen / 2];
+  __shared__ __align__(16) float red[8][32][G * 4];
+  __shared__ float stat[G][2];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float ks = ksc ? ksc[kh] : 1.0f;
+  const float vs = vsc ? vsc[kh] : 1.0f;
+  const int64_t head_off = ((b * Hk + kh) * (int64_t)max_seq + s0) * 128;
+  const uint8_t* kbase = kc + head_off;
+  const uint8_t* vbase = vc + head_off;
+
+  // ---- query pairs matching the K decode order
+  const int dq = t & 3;
+  uint32_t qp[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride + (int64_t)(kh * G + g) * 128 +
+                                                   32 * dq);
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u4_t v = qr[i];
+      raw[4 * i] = v[0];
+      raw[4 * i + 1] = v[1];
+      raw[4 * i + 2] = v[2];
+      raw[4 * i + 3] = v[3];
+    }
+    // K dword j holds dims 4j..4j+3 -> pairs (4j, 4j+2), (4j+1, 4j+3)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t a = raw[2 * j], c = raw[2 * j + 1];
+      qp[g][2 * j] = (a & 0xFFFFu) | (c << 16);
+      qp[g][2 * j + 1] = (a >> 16) | (c & 0xFFFF0000u);
+    }
+  }
+
+  // ---- QK^T
+  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
+#pragma unroll 1
+  for (int pass = 0; pass < kMaxSplitLen / 64; ++pass) {
+    const int p = pass * 64 + (t >> 2);
+    float acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = 0.f;
+    if (p < n) {
+      const u4_t* kr = reinterpret_cast<const u4_t*>(kbase + (int64_t)p * 128 + 32 * dq);
+      const u4_t k0 = __builtin_nontemporal_load(kr);
+      const u4_t k1 = __builtin_nontemporal_load(kr + 1);
+      uint32_t kw[8] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t h02, h13;
+        fp8x4_to_h2_div256(kw[j], h02, h13);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          acc[g] = __builtin_amdgcn_fdot2(as_h2(h02), as_h2(qp[g][2 * j]), acc[g], false);
+          acc[g] = __builtin_amdgcn_fdot2(as_h2(h13), as_h2(qp[g][2 * j + 1]), acc[g], false);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      acc[g] += dpp<kDppQuadXor1>(acc[g]);
+      acc[g] += dpp<kDppQuadXor2>(acc[g]);
+    }
+    if (dq == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[g][p] = (p < n) ? acc[g] * sscale : -INFINITY;
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax statistics and fp16 probabilities
+  for (int g = wave; g < G; g += 4) {
+    const f4_t v = *reinterpret_cast<const f4_t*>(&sc[g][4 * lane]);
+    const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = (m == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - m)));
+    const float l = wave_sum((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    pp[g][2 * lane] = (uint32_t)f2h(pr[0]) | ((uint32_t)f2h(pr[1]) << 16);
+    pp[g][2 * lane + 1] = (uint32_t)f2h(pr[2]) | ((uint32_t)f2h(pr[3]) << 16);
+    if (lane == 0) {
+      stat[g][0] = m;
+      stat[g][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- P V
+  const int d4 = lane & 31, half = lane >> 5;
+  float o[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[g][j] = 0.f;
+  for (int i = 2 * wave + half; 2 * i < n; i += 8) {
+    const int r0 = 2 * i, r1 = min(2 * i + 1, n - 1);
+    const uint32_t a = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)r0 * 128 + 4 * d4);
+    const uint32_t c = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)r1 * 128 + 4 * d4);
+    // (a0 a1 c0 c1) and (a2 a3 c2 c3): decode gives (a_d, c_d) pairs per dim
+    const uint32_t x0 = __builtin_amdgcn_perm(c, a, 0x05040100u);
+    const uint32_t x1 = __builtin_amdgcn_perm(c, a, 0x07060302u);
+    uint32_t h0, h1, h2, h3;
+    fp8x4_to_h2_div256(x0, h0, h1);
+    fp8x4_to_h2_div256(x1, h2, h3);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const h2_t pg = as_h2(pp[g][i]);
+      o[g][0] = __builtin_amdgcn_fdot2(as_h2(h0), pg, o[g][0], false);
+      o[g][1] = __builtin_amdgcn_fdot2(as_h2(h1), pg, o[g][1], false);
+      o[g][2] = __builtin_amdgcn_fdot2(as_h2(h2), pg, o[g][2], false);
+      o[g][3] = __builtin_amdgcn_fdot2(as_h2(h3), pg, o[g][3], false);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[2 * wave + half][d4][4 * g + j] = o[g][j];
+  __syncthreads();
+
+  const float oscale = vs * 256.0f;
+  float* out = part + ((b * H + (int64_t)kh * G) * nsplit + sp) * kPart;
+  for (int e = t; e < G * 128; e += 256) {
+    const int g = e >> 7, d = e & 127;
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s += red[r][d >> 2][4 * g + (d & 3)];
+    out[(int64_t)g * nsplit * kPart + 2 + d] = s * oscale;
+  }
+  if (t < G) {
+    out[(int64_t)t * nsplit * kPart + 0] = stat[t][0];
+    out[(int64_t)t * nsplit * kPart + 1] = stat[t][1];
+  }
+}
+
+// grid (ceil(H/16), B), 64 threads: lane -> head blockIdx.x*16 + lane/4,
+// 32-dim chunk lane%4.
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ part,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t out_stride, int H, int nsplit,
+                                                          int fwht) {
+  const int h = blockIdx.x * 16 + (threadIdx.x >> 2);
+  const int c = threadIdx.x & 3;
+  const int64_t b = blockIdx.y;
+  if (h >= H) return;
+  const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pb[(int64_t)s * kPart]);
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  float Lsum = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float* ps = pb + (int64_t)s * kPart;
+      const float ms = ps[0];
+      if (ms == -INFINITY) continue;
+      const float wgt = __expf(ms - M);
+      Lsum = __builtin_fmaf(wgt, ps[1], Lsum);
+      const float* os = ps + 2 + 32 * c;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] = __builtin_fmaf(wgt, os[i], acc[i]);
+    }
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] *= inv;
+  if (fwht) fwht32(acc);
+  uint16_t* dst = out + b * out_stride + (int64_t)h * 128 + 32 * c;
+#pragma unroll
+  for (int i = 0; i < 32; i += 2)
+    *reinterpret_cast<uint32_t*>(dst + i) = (uint32_t)f2h(acc[i]) | ((uint32_t)f2h(acc[i + 1]) << 16);
+}
+
+}  // namespace
+
+int attn_num_splits(int64_t seq_len, int64_t B, int64_t Hk) {
+  if (seq_len < 1) seq_len = 1;
+  const int64_t heads = B * Hk;
+  const int64_t target = 512;  // ~2 workgroups per CU
+  int64_t per = (target + heads - 1) / heads;
+  int64_t S = (seq_len + per - 1) / per;
+  if (S < 32) S = 32;
+  if (S > kMaxSplitLen) S = kMaxSplitLen;
+  return (int)((seq_len + S - 1) / S);
+}
+
+size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit) {
+  return (size_t)B * H * nsplit * kPart * sizeof(float);
+}
+
+int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, const void* v_cache,
+                        const float* k_scale, const float* v_scale, void* out, int64_t out_stride,
+                        int64_t B, int64_t H, int64_t Hk, int64_t max_seq, int64_t seq_len,
+                        const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st) {
+  const int G = (int)(H / Hk);
+  const dim3 grid((unsigned)nsplit, (unsigned)Hk, (unsigned)B);
+  const auto* qp = static_cast<const uint16_t*>(q);
+  const auto* kp = static_cast<const uint8_t*>(k_cache);
+  const auto* vp = static_cast<const uint8_t*>(v_cache);
+#define R4Q_ATTN(GG)                                                                        \
+  case GG:                                                                                  \
+    hipLaunchKernelGGL((attn_partial_kernel<GG>), grid, dim3(256), 0, st, qp, q_stride, kp, vp, \
+                       k_scale, v_scale, ws, (int)H, (int)Hk, (int)max_seq, (int)seq_len,   \
+                       seq_len_dev, nsplit);                                                \
+    break;
+  switch (G) {
+    R4Q_ATTN(1)
+    R4Q_ATTN(2)
+    R4Q_ATTN(4)
+    R4Q_ATTN(5)
+    R4Q_ATTN(8)
+    default:
+      return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
+  }
+#undef R4Q_ATTN
+  R4Q_TRY(launch_status("flash_decode partial"));
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((H + 15) / 16), (unsigned)B), dim3(64),
+                     0, st, ws, static_cast<uint16_t*>(out), out_stride, (int)H, nsplit, fwht);
+  return launch_status("flash_decode combine");
+}
+
+int DevBuf::reserve(size_t need) {
+  if (need <= bytes) return R4Q_OK;
+  if (ptr) {
+    (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  const size_t cap = (need + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
+  if (hipMalloc(&ptr, cap) != hipSuccess) {
+    ptr = nullptr;
+    return fail(R4Q_ENOMEM, "hipMalloc(%zu) failed", cap);
+  }
+  bytes = cap;
+  return R4Q_OK;
+}
+
+void DevBuf::release() {
+  if (ptr) (void)hipFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+}
+
+}  // namespace r4q
+
+extern "C" int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
+                                const void* k_cache, const void* v_cache, const float* k_scale,
+                                const float* v_scale, void* out, int64_t B, int64_t H, int64_t Hk,
+                                int64_t D, int64_t max_seq, int64_t seq_len, int fwht,
+                                void* stream) {
+  R4Q_REQUIRE(ctx, "flash_decode: null context");
+  R4Q_REQUIRE(q && k_cache && v_cache && out, "flash_decode: null pointer");
+  R4Q_REQUIRE(D == 128, "flash_decode: head_dim must be 128");
+  R4Q_REQUIRE(B >= 1 && H >= 1 && Hk >= 1 && H % Hk == 0, "flash_decode: bad head counts");
+  R4Q_REQUIRE(seq_len >= 1 && seq_len <= max_seq, "flash_decode: seq_len %lld outside [1, %lld]",
+              (long long)seq_len, (long long)max_seq);
+  R4Q_REQUIRE(q_stride >= H * D && (q_stride % 8) == 0 &&
+                  (reinterpret_cast<uintptr_t>(q) & 15) == 0,
+              "flash_decode: q rows must be 16-byte aligned with stride >= H*D");
+  const int nsplit = r4q::attn_num_splits(seq_len, B, Hk);
+  R4Q_TRY(ctx->attn.reserve(r4q::attn_ws_bytes(B, H, nsplit)));
+  return r4q::launch_flash_decode(q, q_stride, k_cache, v_cache, k_scale, v_scale, out, H * D, B,
+                                  H, Hk, max_seq, seq_len, nullptr, nsplit, fwht,
+                                  static_cast<float*>(ctx->attn.ptr), r4q::as_stream(stream));
+}

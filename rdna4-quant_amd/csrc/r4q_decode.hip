@@ -1,0 +1,471 @@
+// Decode-step orchestration: one token (or B tokens, one per sequence)
+// through every layer, the LM head, on-device greedy sampling, hipGraph
+// capture/replay and the per-category HIP-event profile.
+//
+// Replaces int4_decode_step / int4_decode_step_logits (hip:2343-2595),
+// int4_decode_bench (hip:2601-2795), int4_decode_bench_graph (hip:2801-3041),
+// int4_decode_profile (hip:3047-3273) and int4_decode_loop (hip:3284-3466).
+//
+// Per layer (same dataflow as the reference, hip:2474-2524):
+//   rot -> QKV linear -> QK-norm + RoPE + FP8 KV write -> flash-decode
+//   (+FWHT) -> O linear -> residual + post-norm + FWHT -> gate/up linear ->
+//   SiLU-gate + FWHT -> down linear -> residual + next layer's input norm +
+//   FWHT.
+// The graph path keeps the position, sequence length and step counter in
+// device memory; argmax, the embedding gather and the position advance run
+// inside the graph, so replaying N tokens needs no host work per token.
+#include <string.h>
+
+#include <vector>
+
+#include "r4q_ctx.hpp"
+#include "r4q_device.hpp"
+#include "r4q_gemv.hpp"
+#include "r4q_host.hpp"
+#include "r4q_kernels.hpp"
+
+namespace r4q {
+
+struct GraphCache {
+  hipStream_t stream = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<uint8_t> key;
+  ~GraphCache() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+void destroy_graphs(r4q_ctx* ctx) {
+  delete ctx->graphs;
+  ctx->graphs = nullptr;
+}
+
+namespace {
+
+// Device state words (ctx->misc): position, sequence length, step counter.
+enum { kPos = 0, kSeq = 1, kStep = 2, kStateWords = 4 };
+
+struct Dims {
+  int L, H, Hk, hd, D, I, qkvN, qd;
+  float eps;
+  int max_seq;
+};
+
+struct Bufs {
+  uint16_t *h, *r, *rot, *qkv, *o, *gu, *y, *d, *logits;
+  float* attn;
+  int* state;
+  int64_t* ids;
+  float* amax;  // argmax partials
+};
+
+constexpr int kArgmaxBlocks = 64;
+
+int validate(const r4q_model* m, int64_t B, Dims& dm) {
+  R4Q_REQUIRE(m && m->layers, "decode: null model");
+  R4Q_REQUIRE(B >= 1 && B <= 64, "decode: batch must be in [1, 64] (got %lld)", (long long)B);
+  dm.L = m->n_layers;
+  dm.H = m->n_heads;
+  dm.Hk = m->n_kv_heads;
+  dm.hd = m->head_dim;
+  dm.D = m->hidden;
+  dm.I = m->inter;
+  dm.eps = m->eps;
+  dm.max_seq = m->max_seq;
+  R4Q_REQUIRE(dm.L >= 1 && dm.H >= 1 && dm.Hk >= 1 && dm.H % dm.Hk == 0,
+              "decode: bad layer/head counts");
+  R4Q_REQUIRE(dm.hd == 128, "decode: head_dim must be 128");
+  R4Q_REQUIRE(dm.D % 32 == 0 && dm.I % 32 == 0 && dm.D > 0 && dm.I > 0,
+              "decode: hidden and intermediate sizes must be multiples of 32");
+  R4Q_REQUIRE(m->rope_cos && m->rope_sin && m->rope_len >= 1, "decode: missing RoPE tables");
+  dm.qd = dm.H * dm.hd;
+  dm.qkvN = (dm.H + 2 * dm.Hk) * dm.hd;
+  for (int li = 0; li < dm.L; ++li) {
+    const r4q_layer& y = m->layers[li];
+    R4Q_REQUIRE(y.qkv_N == dm.qkvN && y.o_N == dm.D && y.gu_N == 2 * (int64_t)dm.I &&
+                    y.down_N == dm.D,
+                "decode: layer %d output sizes do not match the model dims", li);
+    R4Q_TRY(gemv_check(y.qkv_w, y.qkv_w, y.qkv_s, y.qkv_w, y.qkv_N, dm.D, y.qkv_bits));
+    R4Q_TRY(gemv_check(y.o_w, y.o_w, y.o_s, y.o_w, y.o_N, dm.qd, y.o_bits));
+    R4Q_TRY(gemv_check(y.gu_w, y.gu_w, y.gu_s, y.gu_w, y.gu_N, dm.D, y.gu_bits));
+    R4Q_TRY(gemv_check(y.down_w, y.down_w, y.down_s, y.down_w, y.down_N, dm.I, y.down_bits));
+    R4Q_REQUIRE(y.in_norm && y.post_norm && y.q_norm && y.k_norm && y.k_cache && y.v_cache,
+                "decode: layer %d has a null norm weight or cache", li);
+  }
+  if (m->final_norm) {
+    R4Q_REQUIRE(m->lm_K == dm.D, "decode: lm_K must equal hidden");
+    R4Q_TRY(gemv_check(m->lm_w, m->lm_w, m->lm_s, m->lm_w, m->lm_N, m->lm_K, m->lm_bits));
+  }
+  return R4Q_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsplit, Bufs& bf) {
+  const size_t D = dm.D, I = dm.I;
+  const size_t lmN = m->final_norm ? (size_t)m->lm_N : 0;
+  const size_t rotw = dm.qd > dm.D ? dm.qd : dm.D;
+  const size_t sizes[] = {B * D, B * D, B * rotw, B * (size_t)dm.qkvN, B * D, B * 2 * I,
+                          B * I, B * D, B * lmN};
+  size_t total = 0;
+  for (size_t s : sizes) total += align256(s * 2);
+  R4Q_TRY(ctx->step.reserve(total));
+  uint16_t** dst[] = {&bf.h, &bf.r, &bf.rot, &bf.qkv, &bf.o, &bf.gu, &bf.y, &bf.d, &bf.logits};
+  uint8_t* p = static_cast<uint8_t*>(ctx->step.ptr);
+  for (int i = 0; i < 9; ++i) {
+    *dst[i] = reinterpret_cast<uint16_t*>(p);
+    p += align256(sizes[i] * 2);
+  }
+  R4Q_TRY(ctx->attn.reserve(attn_ws_bytes(B, dm.H, nsplit)));
+  bf.attn = static_cast<float*>(ctx->attn.ptr);
+  const size_t misc = align256(kStateWords * 4) + align256(B * 8) +
+                      align256((size_t)B * kArgmaxBlocks * 8);
+  R4Q_TRY(ctx->misc.reserve(misc));
+  uint8_t* q = static_cast<uint8_t*>(ctx->misc.ptr);
+  bf.state = reinterpret_cast<int*>(q);
+  bf.ids = reinterpret_cast<int64_t*>(q + align256(kStateWords * 4));
+  bf.amax = reinterpret_cast<float*>(q + align256(kStateWords * 4) + align256(B * 8));
+  return R4Q_OK;
+}
+
+int linear(const void* x, const void* w, const void* s, void* y, int64_t B, int64_t N, int64_t K,
+           int bits, hipStream_t st) {
+  if (B == 1) return gemv_launch(x, w, s, y, N, K, bits, st);
+  return gemm_launch(x, w, s, y, B, N, K, bits, st);
+}
+
+// Optional event recorder for the per-category profile.
+struct Prof {
+  std::vector<hipEvent_t>* ev = nullptr;
+  void mark(hipStream_t st) {
+    if (!ev) return;
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    (void)hipEventRecord(e, st);
+    ev->push_back(e);
+  }
+};
+
+// Enqueues one decode step for B rows.  pos_dev/seq_dev: device-held
+// position and length (graph replay), else pos_host.  Input hidden states
+// must already be in bf.h.
+int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host,
+                 const int* pos_dev, const int* seq_dev, int nsplit, const Bufs& bf, bool logits,
+                 hipStream_t st, Prof prof = Prof()) {
+  const int64_t D = dm.D, I = dm.I;
+  const float eps = dm.eps;
+  prof.mark(st);
+  R4Q_TRY(launch_rownorm(2, bf.h, nullptr, m->layers[0].in_norm, bf.rot, nullptr, B, D, eps, st));
+  for (int li = 0; li < dm.L; ++li) {
+    const r4q_layer& y = m->layers[li];
+    prof.mark(st);
+    R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st));
+    prof.mark(st);
+    R4Q_TRY(launch_head_norm_rope_kv(bf.qkv, dm.qkvN, y.q_norm, y.k_norm, bf.qkv, dm.qkvN,
+                                     y.k_cache, y.v_cache, y.k_scale, y.v_scale, m->rope_cos,
+                                     m->rope_sin, B, dm.H, dm.Hk, eps, dm.max_seq, pos_host,
+                                     pos_dev, st));
+    prof.mark(st);
+    R4Q_TRY(launch_flash_decode(bf.qkv, dm.qkvN, y.k_cache, y.v_cache, y.k_scale, y.v_scale,
+                                bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
+                                nsplit, 1, bf.attn, st));
+    prof.mark(st);
+    R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
+    prof.mark(st);
+    R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
+    prof.mark(st);
+    R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
+    prof.mark(st);
+    R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
+    R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
+    prof.mark(st);
+    const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm : m->layers[0].in_norm;
+    R4Q_TRY(launch_rownorm(3, bf.d, bf.r, nxt, bf.rot, bf.h, B, D, eps, st));
+  }
+  prof.mark(st);
+  if (logits) {
+    R4Q_TRY(launch_rownorm(2, bf.h, nullptr, m->final_norm, bf.rot, nullptr, B, D, eps, st));
+    R4Q_TRY(linear(bf.rot, m->lm_w, m->lm_s, bf.logits, B, m->lm_N, m->lm_K, m->lm_bits, st));
+  }
+  prof.mark(st);
+  return R4Q_OK;
+}
+
+// ----------------------------------------------------- on-device sampling
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Stage 1: per (block, row) max and first index of the max.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const uint16_t* __restrict__ logits,
+                                                             int64_t V, float* __restrict__ part) {
+  const int64_t b = blockIdx.y;
+  const int64_t per = (V + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = blockIdx.x * per, hi = min(V, lo + per);
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const float v = h2f(logits[b * V + i]);
+    if (better(v, (int)i, bv, bi)) {
+      bv = v;
+      bi = (int)i;
+    }
+  }
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s && better(sv[threadIdx.x + s], si[threadIdx.x + s], sv[threadIdx.x],
+                                  si[threadIdx.x])) {
+      sv[threadIdx.x] = sv[threadIdx.x + s];
+      si[threadIdx.x] = si[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    part[(b * gridDim.x + blockIdx.x) * 2] = sv[0];
+    part[(b * gridDim.x + blockIdx.x) * 2 + 1] = __int_as_float(si[0]);
+  }
+}
+
+// Stage 2 (one block per row): final argmax, token id out, embedding gather
+// into the next step's hidden state.
+__global__ __launch_bounds__(256) void argmax_embed_kernel(
+    const float* __restrict__ part, int nblk, const uint16_t* __restrict__ embed, int64_t vocab,
+    int D, uint16_t* __restrict__ h, int64_t* __restrict__ ids, int64_t* __restrict__ tokens_out,
+    const int* __restrict__ state, int step_host, int B) {
+  const int b = blockIdx.x;
+  __shared__ int tok;
+  if (threadIdx.x == 0) {
+    float bv = -INFINITY;
+    int bi = 0;
+    bool any = false;
+    for (int k = 0; k < nblk; ++k) {
+      const float v = part[(b * nblk + k) * 2];
+      const int i = __float_as_int(part[(b * nblk + k) * 2 + 1]);
+      if (i == 0x7FFFFFFF) continue;
+      if (!any || better(v, i, bv, bi)) {
+        bv = v;
+        bi = i;
+        any = true;
+      }
+    }
+    if (bi >= vocab) bi = 0;
+    tok = bi;
+    ids[b] = bi;
+    const int step = state ? state[kStep] : step_host;
+    if (tokens_out) tokens_out[(int64_t)step * B + b] = bi;
+  }
+  __syncthreads();
+  const u4_t* src = reinterpret_cast<const u4_t*>(embed + (int64_t)tok * D);
+  u4_t* dst = reinterpret_cast<u4_t*>(h + (int64_t)b * D);
+  for (int i = threadIdx.x; i < D / 8; i += blockDim.x) dst[i] = src[i];
+}
+
+__global__ void set_state_kernel(int* state, int pos) {
+  state[kPos] = pos;
+  state[kSeq] = pos + 1;
+  state[kStep] = 0;
+}
+
+__global__ void advance_kernel(int* state) {
+  state[kPos] += 1;
+  state[kSeq] = state[kPos] + 1;
+  state[kStep] += 1;
+}
+
+int enqueue_sample(const r4q_model* m, const Dims& dm, int64_t B, const Bufs& bf,
+                   int64_t* tokens_out, bool device_step, int step_host, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, (unsigned)B), dim3(256), 0, st,
+                     bf.logits, m->lm_N, bf.amax);
+  R4Q_TRY(launch_status("argmax"));
+  hipLaunchKernelGGL(argmax_embed_kernel, dim3((unsigned)B), dim3(256), 0, st, bf.amax,
+                     kArgmaxBlocks, static_cast<const uint16_t*>(m->embed), m->vocab, dm.D, bf.h,
+                     bf.ids, tokens_out, device_step ? bf.state : nullptr, step_host, (int)B);
+  R4Q_TRY(launch_status("argmax_embed"));
+  if (device_step) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, bf.state);
+    R4Q_TRY(launch_status("advance"));
+  }
+  return R4Q_OK;
+}
+
+int check_positions(const r4q_model* m, int64_t first, int64_t count) {
+  R4Q_REQUIRE(first >= 0 && count >= 1, "decode: bad position range");
+  R4Q_REQUIRE(first + count <= m->max_seq,
+              "decode: positions up to %lld exceed the KV cache (max_seq %d)",
+              (long long)(first + count - 1), m->max_seq);
+  R4Q_REQUIRE(first + count <= m->rope_len,
+              "decode: positions up to %lld exceed the RoPE table (%d rows)",
+              (long long)(first + count - 1), m->rope_len);
+  return R4Q_OK;
+}
+
+// Key of a captured graph: model struct, layer table and launch shape.
+std::vector<uint8_t> graph_key(const r4q_model* m, int64_t B, int nsplit, const void* tokens_out,
+                               const Bufs& bf) {
+  std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 64);
+  uint8_t* p = k.data();
+  memcpy(p, m, sizeof(r4q_model));
+  p += sizeof(r4q_model);
+  memcpy(p, m->layers, sizeof(r4q_layer) * m->n_layers);
+  p += sizeof(r4q_layer) * m->n_layers;
+  const void* extra[] = {tokens_out, bf.h, bf.attn, bf.state};
+  memcpy(p, &B, 8);
+  memcpy(p + 8, &nsplit, 4);
+  memcpy(p + 16, extra, sizeof(extra));
+  return k;
+}
+
+}  // namespace
+}  // namespace r4q
+
+using namespace r4q;
+
+extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
+                               int64_t pos, void* hidden_out, void* logits, void* stream) {
+  R4Q_REQUIRE(ctx && hidden_in, "decode_step: null context or input");
+  Dims dm;
+  R4Q_TRY(validate(m, B, dm));
+  R4Q_TRY(check_positions(m, pos, 1));
+  R4Q_REQUIRE(!logits || m->final_norm, "decode_step: logits requested but the model has no LM head");
+  const int nsplit = attn_num_splits(pos + 1, B, dm.Hk);
+  Bufs bf;
+  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
+  hipStream_t st = as_stream(stream);
+  R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
+  R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, logits != nullptr, st));
+  if (logits)
+    R4Q_HIP_TRY(hipMemcpyAsync(logits, bf.logits, (size_t)B * m->lm_N * 2,
+                               hipMemcpyDeviceToDevice, st));
+  if (hidden_out)
+    R4Q_HIP_TRY(hipMemcpyAsync(hidden_out, bf.h, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
+  return R4Q_OK;
+}
+
+extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
+                                int64_t num_tokens, int64_t start_pos, int use_graph,
+                                void* tokens_out, void* stream) {
+  R4Q_REQUIRE(ctx && hidden_in, "decode_bench: null context or input");
+  Dims dm;
+  R4Q_TRY(validate(m, B, dm));
+  R4Q_REQUIRE(m->final_norm && m->embed && m->vocab >= m->lm_N,
+              "decode_bench: greedy decoding needs an LM head and an embedding table");
+  R4Q_REQUIRE(num_tokens >= 1, "decode_bench: num_tokens must be >= 1");
+  R4Q_TRY(check_positions(m, start_pos, num_tokens));
+  const int nsplit = attn_num_splits(start_pos + num_tokens, B, dm.Hk);
+  Bufs bf;
+  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
+  hipStream_t st = as_stream(stream);
+  int64_t* toks = static_cast<int64_t*>(tokens_out);
+  R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
+  if (!use_graph) {
+    for (int64_t t = 0; t < num_tokens; ++t) {
+      const int64_t pos = start_pos + t;
+      R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, attn_num_splits(pos + 1, B, dm.Hk), bf,
+                           true, st));
+      R4Q_TRY(enqueue_sample(m, dm, B, bf, toks, false, (int)t, st));
+    }
+    return R4Q_OK;
+  }
+  // ---- graph path
+  if (!ctx->graphs) ctx->graphs = new GraphCache();
+  GraphCache& gc = *ctx->graphs;
+  if (!gc.stream) R4Q_HIP_TRY(hipStreamCreateWithFlags(&gc.stream, hipStreamNonBlocking));
+  hipEvent_t ev;
+  R4Q_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  (void)hipEventRecord(ev, st);
+  (void)hipStreamWaitEvent(gc.stream, ev, 0);
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, gc.stream, bf.state, (int)start_pos);
+  int rc = launch_status("set_state");
+  std::vector<uint8_t> key = graph_key(m, B, nsplit, tokens_out, bf);
+  if (rc == R4Q_OK && (!gc.exec || gc.key != key)) {
+    if (gc.exec) {
+      (void)hipGraphExecDestroy(gc.exec);
+      gc.exec = nullptr;
+    }
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamBeginCapture(gc.stream, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+      rc = fail(R4Q_EHIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    } else {
+      const int* pos_dev = bf.state + kPos;
+      const int* seq_dev = bf.state + kSeq;
+      int rc1 = enqueue_step(m, dm, B, start_pos, pos_dev, seq_dev, nsplit, bf, true, gc.stream);
+      if (rc1 == R4Q_OK) rc1 = enqueue_sample(m, dm, B, bf, toks, true, 0, gc.stream);
+      e = hipStreamEndCapture(gc.stream, &graph);
+      if (rc1 != R4Q_OK) rc = rc1;
+      else if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+      else {
+        e = hipGraphInstantiate(&gc.exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+          gc.exec = nullptr;
+          rc = fail(R4Q_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+        } else {
+          gc.key = key;
+        }
+      }
+      if (graph) (void)hipGraphDestroy(graph);
+    }
+  }
+  for (int64_t t = 0; rc == R4Q_OK && t < num_tokens; ++t) {
+    const hipError_t e = hipGraphLaunch(gc.exec, gc.stream);
+    if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+  }
+  (void)hipEventRecord(ev, gc.stream);
+  (void)hipStreamWaitEvent(st, ev, 0);
+  (void)hipEventDestroy(ev);
+  return rc;
+}
+
+extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                                  int64_t pos, float* out_ms, void* stream) {
+  R4Q_REQUIRE(ctx && hidden_in && out_ms, "decode_profile: null argument");
+  Dims dm;
+  R4Q_TRY(validate(m, 1, dm));
+  R4Q_TRY(check_positions(m, pos, 1));
+  const int nsplit = attn_num_splits(pos + 1, 1, dm.Hk);
+  Bufs bf;
+  R4Q_TRY(reserve(ctx, m, dm, 1, nsplit, bf));
+  hipStream_t st = as_stream(stream);
+  R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)dm.D * 2, hipMemcpyDeviceToDevice, st));
+  std::vector<hipEvent_t> ev;
+  Prof prof;
+  prof.ev = &ev;
+  int rc = enqueue_step(m, dm, 1, pos, nullptr, nullptr, nsplit, bf, m->final_norm != nullptr, st,
+                        prof);
+  if (rc == R4Q_OK) {
+    (void)hipEventSynchronize(ev.back());
+    // events: start, then per layer 8 marks, then end-of-layers, end
+    float gemv = 0, attn = 0, norm = 0, total = 0, ms = 0;
+    for (int li = 0; li < dm.L; ++li) {
+      hipEvent_t* e = &ev[1 + 8 * li];  // e[0] = before QKV
+      (void)hipEventElapsedTime(&ms, e[0], e[1]); gemv += ms;   // QKV
+      (void)hipEventElapsedTime(&ms, e[1], e[2]); norm += ms;   // QK-norm + RoPE + KV
+      (void)hipEventElapsedTime(&ms, e[2], e[3]); attn += ms;   // flash-decode
+      (void)hipEventElapsedTime(&ms, e[3], e[4]); gemv += ms;   // O
+      (void)hipEventElapsedTime(&ms, e[4], e[5]); norm += ms;   // residual + norm
+      (void)hipEventElapsedTime(&ms, e[5], e[6]); gemv += ms;   // gate/up
+      (void)hipEventElapsedTime(&ms, e[6], e[7]); gemv += ms;   // SiLU + down
+      const hipEvent_t nxt = ev[1 + 8 * (li + 1)];
+      (void)hipEventElapsedTime(&ms, e[7], nxt); norm += ms;    // residual + norm
+    }
+    (void)hipEventElapsedTime(&total, ev.front(), ev.back());
+    out_ms[0] = total;
+    out_ms[1] = gemv;
+    out_ms[2] = attn;
+    out_ms[3] = norm;
+    out_ms[4] = total - gemv - attn - norm;
+  }
+  for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+  return rc;
+}
+
+extern "C" int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* ids, int64_t M,
+                                  void* logits, int write_kv, void* stream) {
+  (void)ctx; (void)m; (void)ids; (void)M; (void)logits; (void)write_kv; (void)stream;
+  return fail(R4Q_EUNSUPPORTED, "prefill_logits: not built yet");
+}

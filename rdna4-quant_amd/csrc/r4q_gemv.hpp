@@ -1,0 +1,20 @@
+// Internal interface of the GEMV translation unit (used by the decode step).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace r4q {
+
+// Validates a batch-1 GEMV request; returns R4Q_OK or an R4Q_E* code.
+int gemv_check(const void* x, const void* w, const void* sz, const void* y, int64_t N,
+               int64_t K, int wbits);
+// Enqueues y = W x on `st` (arguments already validated).
+int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
+                int wbits, hipStream_t st);
+
+// y[M,N] = x[M,K] W^T; rows of x and y contiguous.
+int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
+                int64_t K, int wbits, hipStream_t st);
+
+}  // namespace r4q

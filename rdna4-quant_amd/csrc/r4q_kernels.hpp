@@ -1,0 +1,26 @@
+// Internal launchers shared between translation units (decode step, prefill).
+// Arguments are validated by the callers; these only enqueue work.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace r4q {
+
+// mode: 0 rmsnorm, 1 residual+rmsnorm, 2 rmsnorm+FWHT, 3 residual+rmsnorm+FWHT
+int launch_rownorm(int mode, const void* a, const void* b, const void* w, void* y,
+                   void* res_out, int64_t rows, int64_t D, float eps, hipStream_t st);
+int launch_silu(bool fwht, const void* g, const void* u, void* y, int64_t rows, int64_t I,
+                int64_t in_stride, int64_t out_stride, hipStream_t st);
+int check_head_norm_rope_kv(const void* qkv, const void* qw, const void* kw, const void* q_out,
+                            const void* k_cache, const void* v_cache, const void* cos_t,
+                            const void* sin_t, int64_t B, int64_t H, int64_t Hk, int64_t D,
+                            int64_t max_seq, int64_t pos);
+// pos_dev != nullptr: position read from device memory (graph replay).
+int launch_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw, const void* kw,
+                             void* q_out, int64_t q_out_stride, void* k_cache, void* v_cache,
+                             const float* k_scale, const float* v_scale, const void* cos_t,
+                             const void* sin_t, int64_t B, int64_t H, int64_t Hk, float eps,
+                             int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st);
+
+}  // namespace r4q

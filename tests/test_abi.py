@@ -1,0 +1,87 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point include/r4q.h declares, the ctypes table matches the header, and
+argument validation rejects bad requests before any device work."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import r4q_lib as R
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "r4q.h"
+
+
+def header_functions():
+    txt = HEADER.read_text()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(r4q_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_loads_and_exports_every_header_symbol():
+    L = R.lib()
+    names = header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, f"declared in r4q.h but not exported: {missing}"
+    assert L.r4q_abi_version() == 1
+
+
+def test_ctypes_table_covers_header():
+    names = set(header_functions()) - {"r4q_last_error"}
+    assert names == set(R.SIGNATURES), names ^ set(R.SIGNATURES)
+
+
+def _einval(rc):
+    assert rc == R.R4Q_EINVAL, rc
+    assert R.last_error()
+
+
+def test_gemv_rejects_bad_arguments():
+    L = R.lib()
+    p = C.c_void_p(256)  # never dereferenced: validation fails first
+    _einval(L.r4q_gemv(p, p, p, p, 16, 33, 4, None))       # K % 32
+    _einval(L.r4q_gemv(p, p, p, p, 16, 64, 5, None))       # wbits
+    _einval(L.r4q_gemv(None, p, p, p, 16, 64, 4, None))    # null x
+    _einval(L.r4q_gemv(p, p, None, p, 16, 64, 4, None))    # null sz for INT4
+    _einval(L.r4q_gemv(p, p, p, p, 0, 64, 4, None))        # N == 0
+    _einval(L.r4q_gemv(C.c_void_p(258), p, p, p, 16, 64, 4, None))  # misaligned x
+    assert "wbits" in (L.r4q_gemv(p, p, p, p, 16, 64, 3, None) and R.last_error())
+
+
+def test_codec_rejects_bad_arguments():
+    L = R.lib()
+    p = C.c_void_p(256)
+    _einval(L.r4q_dequant_int4(p, p, p, 4, 48, None))
+    _einval(L.r4q_dequant_int8(p, None, p, 4, 64, None))
+    _einval(L.r4q_fp16_to_fp8(None, p, 16, None))
+    assert L.r4q_fp16_to_fp8(None, None, 0, None) == R.R4Q_OK  # empty is a no-op
+
+
+def test_norm_and_attention_reject_bad_arguments():
+    L = R.lib()
+    p = C.c_void_p(256)
+    _einval(L.r4q_rmsnorm_fwht(p, p, p, 1, 100, C.c_float(1e-6), None))   # D % 32
+    _einval(L.r4q_fwht32(p, p, 31, None))
+    _einval(L.r4q_head_norm_rope_kv(p, 7168, p, p, p, 7168, p, p, None, None, p, p,
+                                    1, 40, 8, 64, C.c_float(1e-6), 16, 3, None))  # D != 128
+    _einval(L.r4q_head_norm_rope_kv(p, 7168, p, p, p, 7168, p, p, None, None, p, p,
+                                    1, 40, 8, 128, C.c_float(1e-6), 16, 16, None))  # pos >= max_seq
+    _einval(L.r4q_flash_decode(None, p, 5120, p, p, None, None, p, 1, 40, 8, 128, 16, 4, 1, None))
+
+
+def test_weight_bits_inference():
+    import int4_hip
+    assert int4_hip.weight_bits(torch.empty(4, 32, dtype=torch.uint8), 64) == 4
+    assert int4_hip.weight_bits(torch.empty(4, 64, dtype=torch.uint8), 64) == 8
+    assert int4_hip.weight_bits(torch.empty(4, 64, dtype=torch.float16), 64) == 16
+    with pytest.raises(ValueError):
+        int4_hip.weight_bits(torch.empty(4, 48, dtype=torch.uint8), 64)
+    with pytest.raises(ValueError):
+        int4_hip.weight_bits(torch.empty(4, 64, dtype=torch.float32), 64)
+
+
+def test_check_raises_runtime_error():
+    with pytest.raises(RuntimeError):
+        R.check(R.R4Q_EINVAL, "probe")

@@ -1,0 +1,136 @@
+"""Decode-step parity: the int4_hip drop-in (decode_step_logits, decode_step,
+decode_bench[_graph], decode_loop, decode_profile) against the oracle, plus
+size-independent properties (graph == eager, batch rows == single rows)."""
+import numpy as np
+import pytest
+import torch
+
+import int4_hip
+import r4q_synth as S
+from conftest import rel_l2
+from decode_util import bench_args, build, layer_args, oracle_step, step_logits
+
+pytestmark = pytest.mark.gpu
+TOL = 5e-3
+
+
+def _hidden(m, seed, rows=1):
+    return (torch.randn(rows, 1, m.D, generator=S.gen(seed)) * 0.5).half()
+
+
+@pytest.mark.parametrize("kv_scale", [False, True])
+def test_small_model_step_vs_oracle(dev, kv_scale):
+    bits = {(0, "o"): 8, (1, "down"): 8, (1, "qkv"): 8}
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=2, vocab=1000, max_seq=64, seed=3, bits=bits,
+              fill=5, kv_scale=kv_scale)
+    h = _hidden(m, 1)
+    pos = 5
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(-1)
+    kc = [m.kc_np[li, 0].copy() for li in range(m.L)]
+    vc = [m.vc_np[li, 0].copy() for li in range(m.L)]
+    _, want = oracle_step(m, h.numpy().reshape(-1), pos, kc, vc)
+    assert rel_l2(logits, want) <= TOL
+    # KV bytes written at pos: V bytes come straight from the QKV projection's
+    # fp16 output, K after norm + RoPE; rounding-order differences in the
+    # projection may move a code by one step, nothing more
+    for li in range(m.L):
+        gk = m.k_caches[li][0, :, pos].cpu().numpy().astype(np.int16)
+        gv = m.v_caches[li][0, :, pos].cpu().numpy().astype(np.int16)
+        assert (gk == kc[li][:, pos]).mean() > 0.95
+        assert (gv == vc[li][:, pos]).mean() > 0.95
+        assert np.array_equal(m.k_caches[li][0, :, :pos].cpu().numpy(), m.kc_np[li, 0, :, :pos])
+
+
+def test_qwen3_width_two_layers_vs_oracle(dev):
+    bits = {(0, "gu"): 8, (1, "down"): 8}
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=4096, max_seq=160, seed=11, bits=bits,
+              fill=100, kv_scale=True)
+    h = _hidden(m, 2)
+    pos = 100
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(-1)
+    kc = [m.kc_np[li, 0].copy() for li in range(m.L)]
+    vc = [m.vc_np[li, 0].copy() for li in range(m.L)]
+    _, want = oracle_step(m, h.numpy().reshape(-1), pos, kc, vc)
+    assert rel_l2(logits, want) <= TOL
+
+
+def test_decode_step_hidden_matches_oracle(dev):
+    m = build(dev, D=256, I=512, H=8, Hk=2, L=3, vocab=64, max_seq=32, seed=5, fill=0)
+    h = _hidden(m, 3)
+    had = torch.zeros(32, 32, dtype=torch.float16, device=dev)
+    out = int4_hip.decode_step(h.to(dev), *layer_args(m, 0), m.k_caches, m.v_caches, had)
+    assert out.shape == (1, 1, m.D)
+    kc = [m.kc_np[li, 0].copy() for li in range(m.L)]
+    vc = [m.vc_np[li, 0].copy() for li in range(m.L)]
+    want, _ = oracle_step(m, h.numpy().reshape(-1), 0, kc, vc)
+    assert rel_l2(out.cpu().float().numpy().reshape(-1), want) <= TOL
+
+
+def test_batch_rows_equal_single_rows(dev):
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=2, vocab=500, max_seq=40, seed=9, batch=3, fill=7)
+    h = _hidden(m, 4, rows=3)
+    batched = step_logits(m, h.to(dev), 7).cpu()
+    for b in range(3):
+        m.k_caches = [torch.from_numpy(m.kc_np[li, b:b + 1].copy()).to(dev) for li in range(m.L)]
+        m.v_caches = [torch.from_numpy(m.vc_np[li, b:b + 1].copy()).to(dev) for li in range(m.L)]
+        single = step_logits(m, h[b:b + 1].to(dev), 7).cpu()
+        assert rel_l2(batched[b], single[0]) <= 1e-3
+
+
+@pytest.mark.parametrize("D,I,H,Hk,vocab", [(256, 512, 4, 2, 300), (5120, 17408, 40, 8, 2048)])
+def test_graph_replay_equals_eager(dev, D, I, H, Hk, vocab):
+    m = build(dev, D=D, I=I, H=H, Hk=Hk, L=2, vocab=vocab, max_seq=96, seed=21, fill=40,
+              bits={(1, "o"): 8})
+    h = _hidden(m, 6).to(dev)
+    n = 12
+    toks_e = int4_hip.decode_loop(m.embed_d, m.final_norm_d, m.lm_w_d, m.lm_s_d, m.vocab, m.D, h, n,
+                                  *layer_args(m, 40), m.k_caches, m.v_caches,
+                                  torch.zeros(32, 32, dtype=torch.float16, device=dev))
+    kc_e = [t.cpu().clone() for t in m.k_caches]
+    m.reset_caches()
+    toks_g = torch.empty(n, 1, dtype=torch.int64, device=dev)
+    int4_hip._bench(h, m.embed_d, n, bench_args(m, 40), True, tokens_out=toks_g)
+    torch.cuda.synchronize()
+    assert torch.equal(toks_e, toks_g.cpu()[:, 0])
+    for a, b in zip(kc_e, m.k_caches):
+        assert torch.equal(a, b.cpu())
+    # a second replay from the same state reuses the captured graph
+    m.reset_caches()
+    toks_g2 = torch.empty(n, 1, dtype=torch.int64, device=dev)
+    int4_hip._bench(h, m.embed_d, n, bench_args(m, 40), True, tokens_out=toks_g2)
+    torch.cuda.synchronize()
+    assert torch.equal(toks_g2, toks_g)
+
+
+def test_decode_loop_matches_host_greedy(dev):
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=2, vocab=300, max_seq=64, seed=31, fill=10)
+    h = _hidden(m, 7).to(dev)
+    n = 8
+    had = torch.zeros(32, 32, dtype=torch.float16, device=dev)
+    toks = int4_hip.decode_loop(m.embed_d, m.final_norm_d, m.lm_w_d, m.lm_s_d, m.vocab, m.D, h, n,
+                                *layer_args(m, 10), m.k_caches, m.v_caches, had)
+    m.reset_caches()
+    hid = h
+    want = []
+    for t in range(n):
+        lg = step_logits(m, hid, 10 + t)
+        tok = int(lg.float().reshape(-1).argmax())
+        want.append(tok)
+        hid = m.embed_d[tok].view(1, 1, m.D).contiguous()
+    assert toks.tolist() == want
+
+
+def test_decode_bench_and_profile_run(dev):
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=2, vocab=300, max_seq=64, seed=41, fill=10)
+    h = _hidden(m, 8).to(dev)
+    int4_hip.decode_bench(h, m.embed_d, 5, *bench_args(m, 10))
+    int4_hip.decode_bench_graph(h, m.embed_d, 5, *bench_args(m, 10))
+    prof = int4_hip.decode_profile(h, m.embed_d, *bench_args(m, 20))
+    assert len(prof) == 5 and prof[0] > 0
+    assert prof[1] + prof[2] + prof[3] <= prof[0] * 1.01
+
+
+def test_decode_rejects_position_beyond_cache(dev):
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=1, vocab=100, max_seq=16, seed=1)
+    with pytest.raises(RuntimeError):
+        step_logits(m, _hidden(m, 1).to(dev), 16)

@@ -1,0 +1,98 @@
+"""GPU parity of the batch-1 GEMV (INT4 / INT8 / FP16) against the oracle.
+Tolerance: rel-L2 <= 5e-3 on the fp16 output (fp32 accumulation)."""
+import numpy as np
+import pytest
+import torch
+
+import int4_hip
+import r4q_oracle as O
+import r4q_synth as S
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 5e-3
+
+
+def _run(dev, bits, N, K, seed):
+    g = S.gen(seed)
+    w, sz = S.weight(N, K, bits, g)
+    x = S.rotated_activation(K, g)[0]
+    y = int4_hip.dbg_gemv(x.to(dev), w.to(dev), None if sz is None else sz.to(dev), N, K)
+    want = O.gemv(x.numpy(), w.numpy(), None if sz is None else sz.numpy(), bits)
+    return y.cpu().numpy(), want, (w, sz, x)
+
+
+@pytest.mark.parametrize("bits,N,K", [
+    (4, 17408, 5120),    # config 0: gate_proj
+    (4, 7168, 5120),     # qkv
+    (4, 34816, 5120),    # gate_up
+    (4, 5120, 17408),    # down (INT4)
+    (8, 5120, 17408),    # down (INT8)
+    (8, 5120, 5120),     # o (INT8)
+    (16, 8192, 5120),    # LM-head slice (FP16)
+])
+def test_gemv_qwen3_shapes(dev, bits, N, K):
+    got, want, _ = _run(dev, bits, N, K, seed=N + K + bits)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("N,K", [(1, 32), (3, 64), (7, 160), (100, 256), (33, 1024), (65, 1536),
+                                 (129, 4096), (5, 10240), (2, 2176 * 8)])
+def test_gemv_ragged_shapes(dev, bits, N, K):
+    got, want, _ = _run(dev, bits, N, K, seed=7 * N + K + bits)
+    assert rel_l2(got, want) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_gemv_one_hot_selects_column_exactly(dev, bits):
+    N, K = 777, 5120
+    g = S.gen(99 + bits)
+    w, sz = S.weight(N, K, bits, g)
+    W = O.dequant(w.numpy(), None if sz is None else sz.numpy(), bits)
+    for k in (0, 31, 32, 4095, 5119):
+        x = torch.zeros(K, dtype=torch.float16)
+        x[k] = 1.0
+        y = int4_hip.dbg_gemv(x.to(dev), w.to(dev), None if sz is None else sz.to(dev), N, K)
+        assert np.array_equal(y.cpu().numpy(), W[:, k]), k
+
+
+def test_gemv_reference_known_answer(dev):
+    """tests/test_kernels.py:129-171: N=K=5120, seed 42, RTN-quantised
+    N(0,1) weights, cosine similarity > 0.99 vs the fp16 dequant matmul."""
+    torch.manual_seed(42)
+    N = K = 5120
+    W = torch.randn(N, K)
+    Wb = W.reshape(N, K // 32, 32)
+    vmin, vmax = Wb.amin(-1, keepdim=True), Wb.amax(-1, keepdim=True)
+    scale = torch.where((vmax - vmin) / 15 > 0, (vmax - vmin) / 15, torch.ones_like(vmin))
+    zp = (-vmin / scale).round().clamp(0, 15)
+    q = ((Wb / scale) + zp).round().clamp(0, 15).to(torch.uint8).reshape(N, K)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
+    sz = S.sz_table(scale.squeeze(-1).half(), zp.squeeze(-1).to(torch.uint8))
+    x = torch.randn(1, K).half()
+    Wd = torch.from_numpy(O.dequant_int4(packed.numpy(), sz.numpy()))
+    ref = (x.float() @ Wd.float().T).squeeze(0)
+    y = int4_hip.dbg_gemv(x.squeeze(0).to(dev), packed.to(dev), sz.to(dev), N, K).cpu().float()
+    cos = torch.nn.functional.cosine_similarity(ref[None], y[None]).item()
+    assert cos > 0.99
+    assert rel_l2(y, ref) <= TOL
+
+
+def test_gemv_zero_point_cancels(dev):
+    """q == zp everywhere -> exactly zero output."""
+    N, K = 64, 5120
+    packed = torch.full((N, K // 2), 0x77, dtype=torch.uint8)
+    sz = S.sz_table(torch.full((N, K // 32), 0.01).half(), torch.full((N, K // 32), 7))
+    x = S.rotated_activation(K, S.gen(1))[0]
+    y = int4_hip.dbg_gemv(x.to(dev), packed.to(dev), sz.to(dev), N, K).cpu().float()
+    assert torch.all(y.abs() < 1e-3)
+
+
+def test_gemv_rejects_bad_k(dev):
+    w = torch.zeros(4, 24, dtype=torch.uint8, device=dev)
+    s = torch.zeros(4, 4, dtype=torch.float16, device=dev)
+    x = torch.zeros(48, dtype=torch.float16, device=dev)
+    with pytest.raises((RuntimeError, ValueError)):
+        int4_hip.dbg_gemv(x, w, s, 4, 48)
