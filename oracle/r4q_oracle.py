@@ -328,12 +328,13 @@ def _head_norm_rope(x16: np.ndarray, w16: np.ndarray, c16, s16, eps: float):
 
 
 def head_norm_rope_kv(qkv16, qw, kw, cos_t, sin_t, pos: int, H: int, Hk: int, D: int,
-                      eps: float, k_scale=None, v_scale=None):
+                      eps: float, k_scale=None, v_scale=None, return_prequant=False):
     """QK RMSNorm + half-split RoPE + FP8 KV codes for one token
     (head_rmsnorm_rope_kv hip:1620-1683).  K bytes are encoded from the
     float32 rotated value times 1/k_scale, V bytes from fp16 V times
     1/v_scale (scale 1 reproduces the reference).
-    Returns (q_out16 [H*D], k_out16 [Hk*D], k_bytes [Hk, D], v_bytes [Hk, D])."""
+    Returns (q_out16 [H*D], k_out16 [Hk*D], k_bytes [Hk, D], v_bytes [Hk, D])
+    and, with return_prequant, the float32 values that were encoded."""
     qkv16 = np.asarray(qkv16, np.float16)
     q = qkv16[: H * D].reshape(H, D)
     k = qkv16[H * D: (H + Hk) * D].reshape(Hk, D)
@@ -349,8 +350,12 @@ def head_norm_rope_kv(qkv16, qw, kw, cos_t, sin_t, pos: int, H: int, Hk: int, D:
     vs = np.ones(Hk, np.float32) if v_scale is None else np.asarray(v_scale, np.float32)
     kinv = (np.float32(1.0) / ks).astype(np.float32)[:, None]
     vinv = (np.float32(1.0) / vs).astype(np.float32)[:, None]
-    kb = fp8_encode((k32 * kinv).astype(np.float32))
-    vb = fp8_encode((v.astype(np.float32) * vinv).astype(np.float32))
+    kpre = (k32 * kinv).astype(np.float32)
+    vpre = (v.astype(np.float32) * vinv).astype(np.float32)
+    kb = fp8_encode(kpre)
+    vb = fp8_encode(vpre)
+    if return_prequant:
+        return q_out, k_out, kb, vb, kpre, vpre
     return q_out, k_out, kb, vb
 
 
@@ -393,12 +398,16 @@ class Layer:
 
 def decode_step(layers, hidden16, pos: int, k_caches, v_caches, *, H, Hk, D, hidden, inter,
                 eps, rope_cos, rope_sin, final_norm=None, lm_w=None, lm_s=None, lm_bits=4,
-                k_scales=None, v_scales=None, trace=None):
+                k_scales=None, v_scales=None, trace=None, forced_kv=None, kv_trace=None):
     """One token through all layers (int4_decode_step hip:2343-2528) and,
     with final_norm, the LM head (int4_decode_step_logits hip:2534-2595).
     Mutates k_caches/v_caches ([Hk, max_seq, D] uint8 per layer) at `pos`.
     Returns (hidden_out16, logits16 or None).  `trace` (list) collects the
-    per-layer hidden states."""
+    per-layer hidden states.  `forced_kv` (per layer (k_bytes, v_bytes)
+    [Hk, D]) replaces the oracle's own FP8 codes at `pos` (teacher forcing
+    of the quantisation decisions); `kv_trace` then receives per layer
+    (own_k, own_v, k_prequant, v_prequant) so callers can check that every
+    forced code differs from the oracle's only at a rounding boundary."""
     h = np.asarray(hidden16, np.float16).reshape(-1)
     L = len(layers)
     rot = rmsnorm_fwht(h, layers[0].in_norm, eps)
@@ -407,8 +416,13 @@ def decode_step(layers, hidden16, pos: int, k_caches, v_caches, *, H, Hk, D, hid
         qkv = gemv(rot, ly.qkv_w, ly.qkv_s, ly.qkv_bits)
         ks = None if k_scales is None else k_scales[li]
         vs = None if v_scales is None else v_scales[li]
-        q_out, _, kb, vb = head_norm_rope_kv(qkv, ly.q_norm, ly.k_norm, rope_cos, rope_sin, pos,
-                                             H, Hk, D, eps, ks, vs)
+        q_out, _, kb, vb, kpre, vpre = head_norm_rope_kv(
+            qkv, ly.q_norm, ly.k_norm, rope_cos, rope_sin, pos, H, Hk, D, eps, ks, vs,
+            return_prequant=True)
+        if kv_trace is not None:
+            kv_trace.append((kb, vb, kpre, vpre))
+        if forced_kv is not None:
+            kb, vb = forced_kv[li]
         k_caches[li][:, pos, :] = kb
         v_caches[li][:, pos, :] = vb
         rot = attention_decode(q_out, k_caches[li], v_caches[li], pos + 1, H, Hk, D, ks, vs,

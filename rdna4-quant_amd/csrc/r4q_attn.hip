@@ -118,6 +118,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
         }
       }
     }
+    dot_dpp_fence();
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       acc[g] += dpp<kDppQuadXor1>(acc[g]);

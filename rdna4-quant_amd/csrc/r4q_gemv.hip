@@ -163,6 +163,7 @@ __device__ __forceinline__ u4_t load_nt(const u4_t* p) {
 // Reduces `v` over aligned groups of `lr` lanes (power of two <= 64); the
 // result is valid in the first lane of each group.
 __device__ __forceinline__ float reduce_lr(float v, int lr) {
+  dot_dpp_fence();
   if (lr >= 2) v += dpp<kDppQuadXor1>(v);
   if (lr >= 4) v += dpp<kDppQuadXor2>(v);
   if (lr >= 8) v += dpp<kDppHalfMirror>(v);
@@ -404,6 +405,7 @@ int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N
 
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st) {
+  if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* yp = static_cast<uint16_t*>(y);
   for (int64_t m = 0; m < M; ++m) R4Q_TRY(gemv_launch(xp + m * K, w, sz, yp + m * N, N, K, wbits, st));

@@ -13,6 +13,14 @@ int gemv_check(const void* x, const void* w, const void* sz, const void* y, int6
 int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                 int wbits, hipStream_t st);
 
+// Row counts up to this use the weight-streaming GEMV path; above it the
+// MFMA tile GEMM with on-the-fly dequantisation.
+constexpr int64_t kSkinnyMaxRows = 16;
+
+// MFMA GEMM (r4q_gemm.hip), arguments validated by the caller.
+int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
+                     int64_t K, int wbits, hipStream_t st);
+
 // y[M,N] = x[M,K] W^T; rows of x and y contiguous.
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st);

@@ -17,10 +17,13 @@ int check_head_norm_rope_kv(const void* qkv, const void* qw, const void* kw, con
                             const void* sin_t, int64_t B, int64_t H, int64_t Hk, int64_t D,
                             int64_t max_seq, int64_t pos);
 // pos_dev != nullptr: position read from device memory (graph replay).
+// prefill_rows: row b is position pos + b of cache sequence 0 (else every
+// row is at `pos` in cache sequence b).  Null caches skip the KV write.
 int launch_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw, const void* kw,
                              void* q_out, int64_t q_out_stride, void* k_cache, void* v_cache,
                              const float* k_scale, const float* v_scale, const void* cos_t,
                              const void* sin_t, int64_t B, int64_t H, int64_t Hk, float eps,
-                             int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st);
+                             int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st,
+                             bool prefill_rows = false);
 
 }  // namespace r4q

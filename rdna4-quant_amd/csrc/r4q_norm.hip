@@ -194,11 +194,14 @@ __global__ __launch_bounds__(64) void head_norm_rope_kv_kernel(
     uint8_t* __restrict__ kc, uint8_t* __restrict__ vc, const float* __restrict__ ksc,
     const float* __restrict__ vsc, const uint16_t* __restrict__ cs,
     const uint16_t* __restrict__ sn, int H, int Hk, float eps, int max_seq, int pos_host,
-    const int* __restrict__ pos_dev) {
+    const int* __restrict__ pos_dev, int row_pos_step, int row_kv_step) {
 #pragma clang fp contract(off)
   const int h = blockIdx.x, l = threadIdx.x;
   const int64_t b = blockIdx.y;
-  const int pos = pos_dev ? *pos_dev : pos_host;
+  // decode: every row at the same position, row b -> cache sequence b;
+  // prefill: row b at position pos + b of cache sequence 0
+  const int pos = (pos_dev ? *pos_dev : pos_host) + (int)b * row_pos_step;
+  const int64_t kvb = b * row_kv_step;
   const uint16_t* row = qkv + b * qkv_stride;
   const float c = h2f_ieee(cs[(int64_t)pos * 64 + l]), s = h2f_ieee(sn[(int64_t)pos * 64 + l]);
   if (h < H + Hk) {
@@ -214,18 +217,18 @@ __global__ __launch_bounds__(64) void head_norm_rope_kv_kernel(
     uint16_t* dst = qo + b * qo_stride + h * 128;
     dst[l] = f2h(lo);
     dst[l + 64] = f2h(hi);
-    if (!isq) {
+    if (!isq && kc) {
       const int kh = h - H;
       const float inv = ksc ? 1.0f / ksc[kh] : 1.0f;
-      uint8_t* kp = kc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
+      uint8_t* kp = kc + ((kvb * Hk + kh) * (int64_t)max_seq + pos) * 128;
       kp[l] = (uint8_t)fp8_encode(lo * inv);
       kp[l + 64] = (uint8_t)fp8_encode(hi * inv);
     }
-  } else {
+  } else if (vc) {
     const int kh = h - H - Hk;
     const uint16_t* src = row + (H + Hk + kh) * 128;
     const float inv = vsc ? 1.0f / vsc[kh] : 1.0f;
-    uint8_t* vp = vc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
+    uint8_t* vp = vc + ((kvb * Hk + kh) * (int64_t)max_seq + pos) * 128;
     vp[l] = (uint8_t)fp8_encode(h2f_ieee(src[l]) * inv);
     vp[l + 64] = (uint8_t)fp8_encode(h2f_ieee(src[l + 64]) * inv);
   }
@@ -306,14 +309,16 @@ int launch_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw
                              void* q_out, int64_t q_out_stride, void* k_cache, void* v_cache,
                              const float* k_scale, const float* v_scale, const void* cos_t,
                              const void* sin_t, int64_t B, int64_t H, int64_t Hk, float eps,
-                             int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st) {
+                             int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st,
+                             bool prefill_rows) {
   hipLaunchKernelGGL(head_norm_rope_kv_kernel, dim3((unsigned)(H + 2 * Hk), (unsigned)B),
                      dim3(64), 0, st, static_cast<const uint16_t*>(qkv), qkv_stride,
                      static_cast<const uint16_t*>(qw), static_cast<const uint16_t*>(kw),
                      static_cast<uint16_t*>(q_out), q_out_stride, static_cast<uint8_t*>(k_cache),
                      static_cast<uint8_t*>(v_cache), k_scale, v_scale,
                      static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t),
-                     (int)H, (int)Hk, eps, (int)max_seq, (int)pos, pos_dev);
+                     (int)H, (int)Hk, eps, (int)max_seq, (int)pos, pos_dev,
+                     prefill_rows ? 1 : 0, prefill_rows ? 0 : 1);
   return launch_status("head_norm_rope_kv");
 }
 

@@ -3,9 +3,10 @@
 Distributions follow the benchmark configurations:
   * INT4 weights: nibbles uniform 0..15 packed two per byte, per-32-block
     scales fp16(|N(0,1)| * 0.01 + 1e-3), zero-points uniform 6..9;
-  * INT8 weights: bytes uniform 0..255, same scales, zero-points uniform
-    126..129 (the INT4 zero-point range 6..9 moved to the centre of the
-    8-bit code range, so INT8 and INT4 layers have the same mean);
+  * INT8 weights: bytes uniform 0..255, the INT4 scale distribution / 16
+    and zero-points uniform 126..129 (the INT4 zero-point range moved to the
+    centre of the 8-bit code range), so INT8 layers dequantise to the same
+    value range and mean as INT4 layers;
   * FP16 weights (embedding / LM head): 0.02 * N(0,1);
   * norm weights: fp16(1 + 0.02 * N(0,1));
   * activations: N(0,1) fp16, passed through the block-diagonal FWHT-32 when
@@ -50,10 +51,12 @@ def int4_weight(N: int, K: int, g: torch.Generator, device="cpu"):
 
 
 def int8_weight(N: int, K: int, g: torch.Generator, device="cpu"):
-    """(q uint8 [N, K], sz fp16 [N, K/16])."""
+    """(q uint8 [N, K], sz fp16 [N, K/16]).  Scales are the INT4 ones / 16 so
+    the dequantised weights span the same range as the INT4 layers
+    ((q - zp) in +-128 instead of +-8)."""
     q = torch.randint(0, 256, (N, K), generator=g, device=device, dtype=torch.uint8)
     nb = K // 32
-    scales = block_scales(N, nb, g, device)
+    scales = (block_scales(N, nb, g, device).float() / 16).half()
     zeros = torch.randint(126, 130, (N, nb), generator=g, device=device)
     return q.contiguous(), sz_table(scales, zeros)
 

@@ -103,7 +103,34 @@ def bench_args(m, start_pos):
                                        m.vocab, m.D, had)
 
 
-def oracle_step(m, hidden16, pos, kc, vc, b=0):
+def gpu_kv_at(m, pos, b=0):
+    """Per layer (k_bytes, v_bytes) [Hk, hd] the GPU wrote at `pos`."""
+    return [(m.k_caches[li][b, :, pos].cpu().numpy(), m.v_caches[li][b, :, pos].cpu().numpy())
+            for li in range(m.L)]
+
+
+def check_forced_kv(forced, kv_trace, rel=2.0 ** -8):
+    """Every GPU KV code that differs from the oracle's own must be the code
+    of a value within `rel` (relative to max(|x|, row rms)) of the oracle's
+    pre-quantisation value x: the difference comes from last-bit rounding
+    upstream of the encoder, never from the encoder or the indexing.
+    Returns the number of differing codes."""
+    n_diff = 0
+    for (gk, gv), (ok, ov, kpre, vpre) in zip(forced, kv_trace):
+        for g, o, x in ((gk, ok, kpre), (gv, ov, vpre)):
+            x = x.astype(np.float64)
+            rms = np.sqrt((x ** 2).mean(axis=-1, keepdims=True))
+            slack = rel * np.maximum(np.abs(x), rms)
+            vlo = O.fp8_decode_ref(O.fp8_encode((x - slack).astype(np.float32)))
+            vhi = O.fp8_decode_ref(O.fp8_encode((x + slack).astype(np.float32)))
+            vg = O.fp8_decode_ref(g)
+            ok_ = (vg >= np.minimum(vlo, vhi)) & (vg <= np.maximum(vlo, vhi))
+            n_diff += int((g != o).sum())
+            assert ok_.all(), f"{int((~ok_).sum())} KV codes not explained by rounding"
+    return n_diff
+
+
+def oracle_step(m, hidden16, pos, kc, vc, b=0, forced_kv=None, kv_trace=None):
     """Oracle decode step for batch row b; kc/vc: per-layer [Hk, max_seq, hd]
     arrays mutated in place.  Returns (hidden, logits)."""
     ks = None if m.k_scales is None else [t.numpy() for t in m.k_scales]
@@ -113,4 +140,5 @@ def oracle_step(m, hidden16, pos, kc, vc, b=0):
                          rope_sin=m.sin.numpy(), final_norm=m.final_norm.numpy(),
                          lm_w=m.lm_w.numpy(),
                          lm_s=None if m.lm_s is None else m.lm_s.numpy().reshape(m.vocab, -1, 2),
-                         lm_bits=m.lm_bits, k_scales=ks, v_scales=vs)
+                         lm_bits=m.lm_bits, k_scales=ks, v_scales=vs, forced_kv=forced_kv,
+                         kv_trace=kv_trace)
