@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode hot path (one JSON line on stdout).
+
+Default workload (N=1): Qwen3-14B-shaped 40-layer decode with random-init
+weights (80% of the 160 projection matrices INT4, 20% INT8 by a seeded mask,
+FP16 embedding and LM head), FP8 E4M3 KV cache prefilled to ctx=2048,
+batch 1, one hipGraph-captured step per token (argmax + embedding gather on
+the device).  A "step" is one decoded token.
+
+Also measured in the same run:
+  * roofline: the config-0 INT4 GEMV (K=5120 -> N=17408), timed with HIP
+    events on the stream the library launches on, cycling 8 weight copies so
+    the 256 MB last-level cache cannot hold them; algorithmic bytes per
+    launch = packed weights + 3 B per 32-element block + x in + y out;
+  * cpu_baseline: the numpy oracle (the reference's dequant + matmul +
+    attention path restated) on the host cores, on one full-width layer at
+    ctx=2048 plus the LM head, extrapolated to 40 layers.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 2048]
+       [--batch 1] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "rdna4-quant_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "INT4 GEMV HBM GB/s (% of peak); decode tok/s at ctx=2048, batch 1"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_model(ctx, extra, batch, dev):
+    import torch
+
+    import int4_hip
+    import r4q_synth as S
+
+    c = S.QWEN3_14B
+    D, I, H, Hk, hd, L, V = c["hidden"], c["inter"], c["heads"], c["kv_heads"], c["head_dim"], \
+        c["layers"], c["vocab"]
+    g = S.gen(4, dev)
+    mask = S.precision_mask(L, seed=4)
+    args = {k: [] for k in ("qkv_w", "qkv_s", "qkv_N", "o_w", "o_s", "o_N", "gu_w", "gu_s", "gu_N",
+                            "down_w", "down_s", "down_N", "in_norm", "post_norm", "q_norm",
+                            "k_norm")}
+    wbytes = 0
+    for li in range(L):
+        bits = {n: mask[(li, n)] for n in ("qkv", "o", "gu", "down")}
+        ly = S.make_layer(D, I, H, Hk, hd, g, device=dev, bits=bits)
+        for k in args:
+            args[k].append(ly[k])
+        for n in ("qkv", "o", "gu", "down"):
+            N = ly[n + "_N"]
+            K = {"qkv": D, "o": H * hd, "gu": D, "down": I}[n]
+            wbytes += N * K * ly[n + "_bits"] // 8 + N * (K // 32) * 3
+        if (li + 1) % 10 == 0:
+            log(f"layer {li + 1}/{L} generated")
+    max_seq = ctx + extra
+    kc, vc = [], []
+    for li in range(L):
+        k = torch.zeros(batch, Hk, max_seq, hd, dtype=torch.uint8, device=dev)
+        v = torch.zeros_like(k)
+        k[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev, batch))
+        v[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev, batch))
+        kc.append(k)
+        vc.append(v)
+    cos, sin = S.rope_tables(hd, max_seq, c["rope_theta"], dev)
+    final_norm = S.norm_weight(D, g, dev)
+    lm_w, _ = S.fp16_weight(V, D, g, dev)
+    embed, _ = S.fp16_weight(V, D, g, dev)
+    torch.cuda.synchronize()
+    m = dict(args=args, kc=kc, vc=vc, cos=cos, sin=sin, final_norm=final_norm, lm_w=lm_w,
+             embed=embed, D=D, I=I, H=H, Hk=Hk, hd=hd, L=L, V=V, eps=c["eps"], mask=mask,
+             max_seq=max_seq, wbytes=wbytes, lm_bytes=V * D * 2)
+    return m
+
+
+def bench_args(m, start_pos):
+    import torch
+    a = m["args"]
+    had = torch.zeros(32, 32, dtype=torch.float16, device=m["lm_w"].device)
+    return (a["qkv_w"], a["qkv_s"], a["qkv_N"], a["o_w"], a["o_s"], a["o_N"], a["gu_w"],
+            a["gu_s"], a["gu_N"], a["down_w"], a["down_s"], a["down_N"], a["in_norm"],
+            a["post_norm"], a["q_norm"], a["k_norm"], m["cos"], m["sin"], start_pos, m["H"],
+            m["Hk"], m["hd"], m["D"], m["I"], m["eps"], m["kc"], m["vc"], m["final_norm"],
+            m["lm_w"], None, m["V"], m["D"], had)
+
+
+def gemv_roofline(dev, iters=200, copies=8):
+    """Average duration of the config-0 INT4 GEMV and its algorithmic GB/s."""
+    import torch
+
+    import int4_hip
+    import r4q_synth as S
+    N, K = 17408, 5120
+    g = S.gen(0, dev)
+    ws = [S.int4_weight(N, K, g, dev) for _ in range(copies)]
+    x = S.rotated_activation(K, g, dev)[0]
+    for w, s in ws:
+        int4_hip.dbg_gemv(x, w, s, N, K)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        w, s = ws[i % copies]
+        int4_hip.dbg_gemv(x, w, s, N, K)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    alg = N * K // 2 + N * (K // 32) * 3 + 2 * K + 2 * N
+    return us, alg
+
+
+def cpu_baseline(m, ctx):
+    """Oracle (numpy) time per token on the host, from one full-width layer at
+    `ctx` plus the LM head, extrapolated to all layers."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import torch
+
+    import r4q_oracle as O
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = 1
+    a = m["args"]
+    li = 0
+    ly = O.Layer(**{n + k: (a[n + k][li].cpu().numpy() if a[n + k][li] is not None else None)
+                    for n in ("qkv", "o", "gu", "down") for k in ("_w", "_s")},
+                 **{n + "_bits": m["mask"][(li, n)] for n in ("qkv", "o", "gu", "down")},
+                 in_norm=a["in_norm"][li].cpu().numpy(), post_norm=a["post_norm"][li].cpu().numpy(),
+                 q_norm=a["q_norm"][li].cpu().numpy(), k_norm=a["k_norm"][li].cpu().numpy())
+    for n in ("qkv", "o", "gu", "down"):
+        s = getattr(ly, n + "_s")
+        if s is not None:
+            setattr(ly, n + "_s", s.reshape(s.shape[0], -1, 2))
+    kc = [m["kc"][li][0].cpu().numpy()]
+    vc = [m["vc"][li][0].cpu().numpy()]
+    h = (torch.randn(m["D"], generator=torch.Generator().manual_seed(1)) * 0.5).half().numpy()
+    cos, sin = m["cos"].cpu().numpy(), m["sin"].cpu().numpy()
+    t0 = time.perf_counter()
+    O.decode_step([ly], h, ctx - 1, kc, vc, H=m["H"], Hk=m["Hk"], D=m["hd"], hidden=m["D"],
+                  inter=m["I"], eps=m["eps"], rope_cos=cos, rope_sin=sin)
+    t_layer = time.perf_counter() - t0
+    lm = m["lm_w"].cpu().numpy()
+    t0 = time.perf_counter()
+    O.gemv(O.rmsnorm_fwht(h, m["final_norm"].cpu().numpy(), m["eps"]), lm, None, 16)
+    t_lm = time.perf_counter() - t0
+    t_tok = m["L"] * t_layer + t_lm
+    return {"value": round(1.0 / t_tok, 5), "unit": "tok/s", "cores": int(threads),
+            "kind": "port",
+            "sample": (f"numpy oracle: 1 full-width layer at ctx={ctx} ({t_layer:.2f} s) x "
+                       f"{m['L']} + FP16 LM head ({t_lm:.2f} s), batch 1")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--ctx", type=int, default=2048)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(one GPU per box); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import int4_hip
+    dev = torch.device("cuda:0")
+    log("building synthetic model")
+    t0 = time.time()
+    m = build_model(args.ctx, args.warmup + args.steps + 8, args.batch, dev)
+    log(f"model ready in {time.time() - t0:.1f} s (weights {m['wbytes'] / 1e9:.2f} GB + "
+        f"LM head {m['lm_bytes'] / 1e9:.2f} GB)")
+    h = (torch.randn(args.batch, 1, m["D"], generator=torch.Generator().manual_seed(1)) * 0.5).half().to(dev)
+
+    # warm-up: capture and replay from ctx - warmup so the timed steps start at ctx
+    wpos = args.ctx - args.warmup
+    int4_hip.decode_bench_graph(h, m["embed"], args.warmup, *bench_args(m, wpos))
+    torch.cuda.synchronize()
+    log(f"warm-up {args.warmup} steps done")
+    t0 = time.perf_counter()
+    int4_hip.decode_bench_graph(h, m["embed"], args.steps, *bench_args(m, args.ctx))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt * 1000.0 / args.steps
+    tok_s = args.batch * args.steps / dt
+    log(f"decode: {ms:.3f} ms/step, {tok_s:.1f} tok/s")
+
+    kv_bytes = m["L"] * 2 * m["Hk"] * m["hd"] * (args.ctx + args.steps // 2) * args.batch
+    step_bytes = m["wbytes"] + m["lm_bytes"] + kv_bytes
+    us, alg = gemv_roofline(dev)
+    gbps = alg / us / 1e3
+    log(f"INT4 GEMV 5120->17408: {us:.2f} us, {gbps:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle (one layer + LM head)")
+        cpu = cpu_baseline(m, args.ctx)
+        log(f"cpu baseline: {cpu['value']} tok/s")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (random-init weights, seeded)",
+        "config": {
+            "workload": (f"Qwen3-14B-shaped 40-layer decode, ctx={args.ctx}, batch {args.batch}, "
+                         "hipGraph step, 80% INT4 / 20% INT8 (seeded mask), FP16 LM head, "
+                         "FP8 E4M3 KV"),
+            "hidden": m["D"], "intermediate": m["I"], "heads": m["H"], "kv_heads": m["Hk"],
+            "head_dim": m["hd"], "layers": m["L"], "vocab": m["V"], "ctx": args.ctx,
+            "batch": args.batch,
+        },
+        "step_bytes": step_bytes,
+        "step_gbps": round(step_bytes / (ms / 1e3) / 1e9, 1),
+        "step_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "int4_gemv_gbps": round(gbps, 1),
+        "roofline": {
+            "kernel": "INT4 GEMV K=5120 -> N=17408 (gemv_xreg_kernel<4,5>)",
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(us, 3),
+            "bytes_per_launch": alg,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

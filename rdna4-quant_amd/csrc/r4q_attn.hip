@@ -1,5 +1,5 @@
 // Split-K flash-decode over the FP8 E4M3 KV cache (GQA), with the log-sum-exp
-// merge and the optional FWHT-32 output rotation in a second pass.
+// merge and the optional FWHT-32 output rotation fused into the same launch.
 //
 // Replaces the reference's launch_flash_decode (hip:1547-1593) with its
 // flash_decode_partial (hip:1326-1412), flash_decode_reduce (hip:1416-1463)
@@ -9,19 +9,27 @@
 // dot4_f32_fp8_fp8 instruction does not exist on gfx950), and K/V carry an
 // optional per-head fp32 scale.
 //
-// Partial pass, one workgroup (4 waves) per (split, kv head, sequence):
+// One workgroup (4 waves) per (split, kv head, sequence) walks its split in
+// 256-position tiles:
+//  * every K and V load of a tile is issued before any arithmetic (one
+//    memory latency per tile);
 //  * QK: 4 lanes per position, each owning 32 head dims; the position's 32 K
 //    bytes arrive in two 128-bit loads and are widened to fp16 by placing the
 //    E4M3 fields into fp16 fields (exact, value / 256); the GQA group's query
 //    heads live in registers as fp16 pairs so every K byte feeds all of them
 //    through v_dot2_f32_f16; the 4 partial dots are combined with DPP.
-//  * scores -> LDS; per-head max, exp and the fp16-rounded probabilities
-//    (pairs of positions) -> LDS.
+//  * scores -> LDS; online softmax per head: tile max, running max/sum and
+//    the rescale factor of earlier tiles, fp16-rounded probabilities of
+//    position pairs -> LDS.
 //  * PV: each lane owns 4 head dims; two positions' V bytes are interleaved
-//    with v_perm so v_dot2 contracts over the position pair; partials are
-//    reduced across half-waves and waves through LDS.
-// Combine pass: m* = max_s m_s; out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s,
-// then FWHT-32 in registers (4 lanes x 32 dims per head).
+//    with v_perm so v_dot2 contracts over the position pair; the running
+//    accumulators are rescaled per tile and reduced across half-waves and
+//    waves through LDS at the end.
+// Merge: the last workgroup to finish for a (sequence, kv head) -- found with
+// a self-resetting arrival counter, no waiting -- combines the (at most 64)
+// splits while they are in cache with 128-bit loads: m* = max_s m_s,
+// out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s, then the FWHT-32 in
+// registers (one thread per 32-dim chunk).
 #include <math.h>
 
 #include "r4q_ctx.hpp"
@@ -31,8 +39,9 @@
 namespace r4q {
 namespace {
 
-constexpr int kMaxSplitLen = 256;
-constexpr int kPart = 130;  // floats per (seq, head, split): m, l, o[128]
+constexpr int kTile = 256;       // positions per tile (scores staged in LDS)
+constexpr int kMaxSplits = 64;   // partials merged by the last workgroup
+constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 
 // Four E4M3 bytes (b0 b1 b2 b3) -> fp16 pairs (b0, b2) and (b1, b3), each
 // value divided by 256 (exact).
@@ -47,20 +56,21 @@ template <int G>
 __global__ __launch_bounds__(256) void attn_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
-    float* __restrict__ part, int H, int Hk, int max_seq, int L_host,
+    float* __restrict__ part, int* __restrict__ counters, uint16_t* __restrict__ outp,
+    int64_t out_stride, int fwht, int H, int Hk, int max_seq, int L_host,
     const int* __restrict__ L_dev, int nsplit) {
   const int sp = blockIdx.x, kh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int L = L_dev ? *L_dev : L_host;
   const int S = (L + nsplit - 1) / nsplit;
   const int s0 = sp * S;
-  const int n = max(0, min(L, s0 + S) - s0);  // <= kMaxSplitLen
+  const int n = max(0, min(L, s0 + S) - s0);
 
   // 128-bit LDS accesses below need 16-byte aligned rows
-  __shared__ __align__(16) float sc[G][kMaxSplitLen];
-  __shared__ __align__(16) uint32_t pp[G][kMaxSplitLen / 2];
+  __shared__ __align__(16) float sc[G][kTile];
+  __shared__ __align__(16) uint32_t pp[G][kTile / 2];
   __shared__ __align__(16) float red[8][32][G * 4];
-  __shared__ float stat[G][2];
+  __shared__ float stat[G][4];  // running max, running sum, tile rescale
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float ks = ksc ? ksc[kh] : 1.0f;
@@ -93,87 +103,127 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
       qp[g][2 * j + 1] = (a >> 16) | (c & 0xFFFF0000u);
     }
   }
-
-  // ---- QK^T
-  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
-#pragma unroll 1
-  for (int pass = 0; pass < kMaxSplitLen / 64; ++pass) {
-    const int p = pass * 64 + (t >> 2);
-    float acc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = 0.f;
-    if (p < n) {
-      const u4_t* kr = reinterpret_cast<const u4_t*>(kbase + (int64_t)p * 128 + 32 * dq);
-      const u4_t k0 = __builtin_nontemporal_load(kr);
-      const u4_t k1 = __builtin_nontemporal_load(kr + 1);
-      uint32_t kw[8] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t h02, h13;
-        fp8x4_to_h2_div256(kw[j], h02, h13);
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          acc[g] = __builtin_amdgcn_fdot2(as_h2(h02), as_h2(qp[g][2 * j]), acc[g], false);
-          acc[g] = __builtin_amdgcn_fdot2(as_h2(h13), as_h2(qp[g][2 * j + 1]), acc[g], false);
-        }
-      }
-    }
-    dot_dpp_fence();
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      acc[g] += dpp<kDppQuadXor1>(acc[g]);
-      acc[g] += dpp<kDppQuadXor2>(acc[g]);
-    }
-    if (dq == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) sc[g][p] = (p < n) ? acc[g] * sscale : -INFINITY;
-    }
+  if (t < G) {
+    stat[t][0] = -INFINITY;
+    stat[t][1] = 0.f;
   }
-  __syncthreads();
 
-  // ---- softmax statistics and fp16 probabilities
-  for (int g = wave; g < G; g += 4) {
-    const f4_t v = *reinterpret_cast<const f4_t*>(&sc[g][4 * lane]);
-    const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = (m == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - m)));
-    const float l = wave_sum((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    pp[g][2 * lane] = (uint32_t)f2h(pr[0]) | ((uint32_t)f2h(pr[1]) << 16);
-    pp[g][2 * lane + 1] = (uint32_t)f2h(pr[2]) | ((uint32_t)f2h(pr[3]) << 16);
-    if (lane == 0) {
-      stat[g][0] = m;
-      stat[g][1] = l;
-    }
-  }
-  __syncthreads();
-
-  // ---- P V
   const int d4 = lane & 31, half = lane >> 5;
   float o[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[g][j] = 0.f;
-  for (int i = 2 * wave + half; 2 * i < n; i += 8) {
-    const int r0 = 2 * i, r1 = min(2 * i + 1, n - 1);
-    const uint32_t a = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)r0 * 128 + 4 * d4);
-    const uint32_t c = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)r1 * 128 + 4 * d4);
-    // (a0 a1 c0 c1) and (a2 a3 c2 c3): decode gives (a_d, c_d) pairs per dim
-    const uint32_t x0 = __builtin_amdgcn_perm(c, a, 0x05040100u);
-    const uint32_t x1 = __builtin_amdgcn_perm(c, a, 0x07060302u);
-    uint32_t h0, h1, h2, h3;
-    fp8x4_to_h2_div256(x0, h0, h1);
-    fp8x4_to_h2_div256(x1, h2, h3);
+
+  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
+  for (int base = 0; base < n; base += kTile) {
+    const int nt = min(kTile, n - base);
+    // ---- issue every K and V load of the tile before any arithmetic, so a
+    // tile costs one memory latency.  Rows past the tile end are clamped to
+    // its last row; their scores become -inf and their probabilities 0.
+    constexpr int kPass = kTile / 64;
+    u4_t kw[kPass][2];
+#pragma unroll
+    for (int pass = 0; pass < kPass; ++pass) {
+      const int p = min(pass * 64 + (t >> 2), nt - 1);
+      const u4_t* kr = reinterpret_cast<const u4_t*>(kbase + (int64_t)(base + p) * 128 + 32 * dq);
+      kw[pass][0] = __builtin_nontemporal_load(kr);
+      kw[pass][1] = __builtin_nontemporal_load(kr + 1);
+    }
+    constexpr int kPairs = kTile / 16;  // pairs per (wave, half) slot
+    uint32_t va[kPairs], vb[kPairs];
+#pragma unroll
+    for (int k = 0; k < kPairs; ++k) {
+      const int i = 2 * wave + half + 8 * k;
+      const int r0 = min(2 * i, nt - 1), r1 = min(2 * i + 1, nt - 1);
+      va[k] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint32_t*>(vbase + (int64_t)(base + r0) * 128 + 4 * d4));
+      vb[k] = __builtin_nontemporal_load(
+          reinterpret_cast<const uint32_t*>(vbase + (int64_t)(base + r1) * 128 + 4 * d4));
+    }
+
+    // ---- Q K^T, 4 lanes per position, 64 positions per pass
+#pragma unroll
+    for (int pass = 0; pass < kPass; ++pass) {
+      const int p = pass * 64 + (t >> 2);
+      float acc[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[g] = 0.f;
+      const uint32_t k8[8] = {kw[pass][0][0], kw[pass][0][1], kw[pass][0][2], kw[pass][0][3],
+                              kw[pass][1][0], kw[pass][1][1], kw[pass][1][2], kw[pass][1][3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t h02, h13;
+        fp8x4_to_h2_div256(k8[j], h02, h13);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          acc[g] = __builtin_amdgcn_fdot2(as_h2(h02), as_h2(qp[g][2 * j]), acc[g], false);
+          acc[g] = __builtin_amdgcn_fdot2(as_h2(h13), as_h2(qp[g][2 * j + 1]), acc[g], false);
+        }
+      }
+      dot_dpp_fence();
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        acc[g] += dpp<kDppQuadXor1>(acc[g]);
+        acc[g] += dpp<kDppQuadXor2>(acc[g]);
+      }
+      if (dq == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g][p] = (p < nt) ? acc[g] * sscale : -INFINITY;
+      }
+    }
+    __syncthreads();
+
+    // ---- online softmax: tile max, rescale of the running state, fp16
+    // probabilities of position pairs
+    for (int g = wave; g < G; g += 4) {
+      const f4_t v = *reinterpret_cast<const f4_t*>(&sc[g][4 * lane]);
+      const float mt = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+      const float mo = stat[g][0];
+      const float mn = fmaxf(mo, mt);
+      const float alpha = (mo == -INFINITY) ? 0.f : __expf(mo - mn);
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[i] = (mn == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - mn)));
+      const float l = wave_sum((pr[0] + pr[1]) + (pr[2] + pr[3]));
+      pp[g][2 * lane] = (uint32_t)f2h(pr[0]) | ((uint32_t)f2h(pr[1]) << 16);
+      pp[g][2 * lane + 1] = (uint32_t)f2h(pr[2]) | ((uint32_t)f2h(pr[3]) << 16);
+      if (lane == 0) {
+        stat[g][0] = mn;
+        stat[g][1] = __builtin_fmaf(stat[g][1], alpha, l);
+        stat[g][2] = alpha;
+      }
+    }
+    __syncthreads();
+
+    // ---- P V: lane d4 owns dims 4*d4 .. 4*d4+3 of position pairs
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const h2_t pg = as_h2(pp[g][i]);
-      o[g][0] = __builtin_amdgcn_fdot2(as_h2(h0), pg, o[g][0], false);
-      o[g][1] = __builtin_amdgcn_fdot2(as_h2(h1), pg, o[g][1], false);
-      o[g][2] = __builtin_amdgcn_fdot2(as_h2(h2), pg, o[g][2], false);
-      o[g][3] = __builtin_amdgcn_fdot2(as_h2(h3), pg, o[g][3], false);
+      const float a = stat[g][2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[g][j] *= a;
     }
+#pragma unroll
+    for (int k = 0; k < kPairs; ++k) {
+      const int i = 2 * wave + half + 8 * k;
+      // (a0 a1 c0 c1) and (a2 a3 c2 c3): decode gives (a_d, c_d) pairs per dim
+      const uint32_t x0 = __builtin_amdgcn_perm(vb[k], va[k], 0x05040100u);
+      const uint32_t x1 = __builtin_amdgcn_perm(vb[k], va[k], 0x07060302u);
+      uint32_t h0, h1, h2, h3;
+      fp8x4_to_h2_div256(x0, h0, h1);
+      fp8x4_to_h2_div256(x1, h2, h3);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const h2_t pg = as_h2(pp[g][i]);
+        o[g][0] = __builtin_amdgcn_fdot2(as_h2(h0), pg, o[g][0], false);
+        o[g][1] = __builtin_amdgcn_fdot2(as_h2(h1), pg, o[g][1], false);
+        o[g][2] = __builtin_amdgcn_fdot2(as_h2(h2), pg, o[g][2], false);
+        o[g][3] = __builtin_amdgcn_fdot2(as_h2(h3), pg, o[g][3], false);
+      }
+    }
+    __syncthreads();  // sc / pp / stat rescale reused by the next tile
   }
+
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -187,68 +237,96 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     float s = 0.f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) s += red[r][d >> 2][4 * g + (d & 3)];
-    out[(int64_t)g * nsplit * kPart + 2 + d] = s * oscale;
+    out[(int64_t)g * nsplit * kPart + 4 + d] = s * oscale;
   }
   if (t < G) {
     out[(int64_t)t * nsplit * kPart + 0] = stat[t][0];
     out[(int64_t)t * nsplit * kPart + 1] = stat[t][1];
   }
-}
 
-// grid (ceil(H/16), B), 64 threads: lane -> head blockIdx.x*16 + lane/4,
-// 32-dim chunk lane%4.
-__global__ __launch_bounds__(64) void attn_combine_kernel(const float* __restrict__ part,
-                                                          uint16_t* __restrict__ out,
-                                                          int64_t out_stride, int H, int nsplit,
-                                                          int fwht) {
-  const int h = blockIdx.x * 16 + (threadIdx.x >> 2);
-  const int c = threadIdx.x & 3;
-  const int64_t b = blockIdx.y;
-  if (h >= H) return;
-  const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, pb[(int64_t)s * kPart]);
-  float acc[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-  float Lsum = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float* ps = pb + (int64_t)s * kPart;
-      const float ms = ps[0];
-      if (ms == -INFINITY) continue;
-      const float wgt = __expf(ms - M);
-      Lsum = __builtin_fmaf(wgt, ps[1], Lsum);
-      const float* os = ps + 2 + 32 * c;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) acc[i] = __builtin_fmaf(wgt, os[i], acc[i]);
-    }
+  // ---- the last workgroup to finish for this (sequence, kv head) merges the
+  // splits: m* = max m_s, out = sum e^(m_s-m*) o_s / sum e^(m_s-m*) l_s.
+  // The counter is reset by that workgroup, so it is zero between launches.
+  __shared__ int last;
+  __threadfence();  // publish this split's partials device-wide
+  __syncthreads();
+  if (t == 0) last = (atomicAdd(&counters[b * Hk + kh], 1) == nsplit - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // see every other split's partials
+  const float* pb = part + (b * H + (int64_t)kh * G) * nsplit * kPart;
+  float* wm = &sc[0][0];               // [G][nsplit] split maxima -> weights
+  float* wl = &sc[0][0] + G * nsplit;  // [G][nsplit] split sums
+  for (int e = t; e < G * nsplit; e += 256) {
+    wm[e] = pb[(int64_t)e * kPart];
+    wl[e] = pb[(int64_t)e * kPart + 1];
   }
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  __syncthreads();
+  if (t < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, wm[t * nsplit + s]);
+    float Ls = 0.f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float ms = wm[t * nsplit + s];
+      const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+      wm[t * nsplit + s] = w;
+      Ls = __builtin_fmaf(w, wl[t * nsplit + s], Ls);
+    }
+    stat[t][1] = Ls;
+  }
+  __syncthreads();
+  float* ostage = &red[0][0][0];  // [G][128]
+  if (t < 32 * G) {
+    const int g = t >> 5, c4 = t & 31;
+    const float* po = pb + (int64_t)g * nsplit * kPart + 4 + 4 * c4;
+    f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int s = 0; s < nsplit; ++s) {
+      const f4_t v = *reinterpret_cast<const f4_t*>(po + (int64_t)s * kPart);
+      const float w = wm[g * nsplit + s];
+      acc[0] = __builtin_fmaf(w, v[0], acc[0]);
+      acc[1] = __builtin_fmaf(w, v[1], acc[1]);
+      acc[2] = __builtin_fmaf(w, v[2], acc[2]);
+      acc[3] = __builtin_fmaf(w, v[3], acc[3]);
+    }
+    const float Ls = stat[g][1];
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] *= inv;
-  if (fwht) fwht32(acc);
-  uint16_t* dst = out + b * out_stride + (int64_t)h * 128 + 32 * c;
+    for (int j = 0; j < 4; ++j) ostage[g * 128 + 4 * c4 + j] = acc[j] * inv;
+  }
+  __syncthreads();
+  if (t < 4 * G) {
+    const int g = t >> 2, c = t & 3;
+    float v[32];
 #pragma unroll
-  for (int i = 0; i < 32; i += 2)
-    *reinterpret_cast<uint32_t*>(dst + i) = (uint32_t)f2h(acc[i]) | ((uint32_t)f2h(acc[i + 1]) << 16);
+    for (int i = 0; i < 32; ++i) v[i] = ostage[g * 128 + 32 * c + i];
+    if (fwht) fwht32(v);
+    uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + g) * 128 + 32 * c;
+#pragma unroll
+    for (int i = 0; i < 32; i += 2)
+      *reinterpret_cast<uint32_t*>(dst + i) = (uint32_t)f2h(v[i]) | ((uint32_t)f2h(v[i + 1]) << 16);
+  }
+  if (t == 0) counters[b * Hk + kh] = 0;
 }
 
 }  // namespace
 
-int attn_num_splits(int64_t seq_len, int64_t B, int64_t Hk) {
-  if (seq_len < 1) seq_len = 1;
-  const int64_t heads = B * Hk;
-  const int64_t target = 512;  // ~2 workgroups per CU
-  int64_t per = (target + heads - 1) / heads;
-  int64_t S = (seq_len + per - 1) / per;
-  if (S < 32) S = 32;
-  if (S > kMaxSplitLen) S = kMaxSplitLen;
-  return (int)((seq_len + S - 1) / S);
+int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
+  // One split per 64 positions of the cache, no more than ~4 workgroups
+  // per CU overall and at most kMaxSplits (the merge cost).  Depends only on
+  // the cache capacity, so a captured graph stays valid as the sequence grows.
+  const int64_t by_len = (cap_len + 63) / 64;
+  const int64_t by_chip = (1024 + B * Hk - 1) / (B * Hk);
+  int64_t n = by_len < by_chip ? by_len : by_chip;
+  if (n > kMaxSplits) n = kMaxSplits;
+  return (int)(n < 1 ? 1 : n);
 }
 
+// Workspace: per-(sequence, kv head) arrival counters, then the partials.
+constexpr size_t kCounterBytes = 64 * 1024;
+
 size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit) {
-  return (size_t)B * H * nsplit * kPart * sizeof(float);
+  return kCounterBytes + (size_t)B * H * nsplit * kPart * sizeof(float);
 }
 
 int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, const void* v_cache,
@@ -256,15 +334,20 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
                         int64_t B, int64_t H, int64_t Hk, int64_t max_seq, int64_t seq_len,
                         const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st) {
   const int G = (int)(H / Hk);
+  if (nsplit < 1 || nsplit > kMaxSplits || B * Hk * 4 > (int64_t)kCounterBytes)
+    return fail(R4Q_EUNSUPPORTED, "flash_decode: %d splits / %lld heads exceed the workspace",
+                nsplit, (long long)(B * Hk));
   const dim3 grid((unsigned)nsplit, (unsigned)Hk, (unsigned)B);
+  int* counters = reinterpret_cast<int*>(ws);
+  float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + kCounterBytes);
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
   const auto* vp = static_cast<const uint8_t*>(v_cache);
 #define R4Q_ATTN(GG)                                                                        \
   case GG:                                                                                  \
     hipLaunchKernelGGL((attn_partial_kernel<GG>), grid, dim3(256), 0, st, qp, q_stride, kp, vp, \
-                       k_scale, v_scale, ws, (int)H, (int)Hk, (int)max_seq, (int)seq_len,   \
-                       seq_len_dev, nsplit);                                                \
+                       k_scale, v_scale, part, counters, static_cast<uint16_t*>(out), out_stride, \
+                       fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len, seq_len_dev, nsplit); \
     break;
   switch (G) {
     R4Q_ATTN(1)
@@ -276,10 +359,7 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
       return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
   }
 #undef R4Q_ATTN
-  R4Q_TRY(launch_status("flash_decode partial"));
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((H + 15) / 16), (unsigned)B), dim3(64),
-                     0, st, ws, static_cast<uint16_t*>(out), out_stride, (int)H, nsplit, fwht);
-  return launch_status("flash_decode combine");
+  return launch_status("flash_decode");
 }
 
 int DevBuf::reserve(size_t need) {
@@ -294,6 +374,9 @@ int DevBuf::reserve(size_t need) {
     ptr = nullptr;
     return fail(R4Q_ENOMEM, "hipMalloc(%zu) failed", cap);
   }
+  // zeroed once: the attention arrival counters rely on it (they are reset
+  // to zero by the kernel that consumes them)
+  if (hipMemset(ptr, 0, cap) != hipSuccess) return fail(R4Q_EHIP, "hipMemset failed");
   bytes = cap;
   return R4Q_OK;
 }

@@ -11,6 +11,9 @@
 //   (+FWHT) -> O linear -> residual + post-norm + FWHT -> gate/up linear ->
 //   SiLU-gate + FWHT -> down linear -> residual + next layer's input norm +
 //   FWHT.
+// Every decode path splits attention by the cache capacity (split length =
+// ceil(len / nsplit), computed on the device), so the eager step, the eager
+// loop and the captured graph run the same arithmetic for a given position.
 // The graph path keeps the position, sequence length and step counter in
 // device memory; argmax, the embedding gather and the position advance run
 // inside the graph, so replaying N tokens needs no host work per token.
@@ -332,7 +335,7 @@ extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hid
   R4Q_TRY(validate(m, B, dm));
   R4Q_TRY(check_positions(m, pos, 1));
   R4Q_REQUIRE(!logits || m->final_norm, "decode_step: logits requested but the model has no LM head");
-  const int nsplit = attn_num_splits(pos + 1, B, dm.Hk);
+  const int nsplit = attn_num_splits(m->max_seq, B, dm.Hk);
   Bufs bf;
   R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
@@ -356,7 +359,7 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
               "decode_bench: greedy decoding needs an LM head and an embedding table");
   R4Q_REQUIRE(num_tokens >= 1, "decode_bench: num_tokens must be >= 1");
   R4Q_TRY(check_positions(m, start_pos, num_tokens));
-  const int nsplit = attn_num_splits(start_pos + num_tokens, B, dm.Hk);
+  const int nsplit = attn_num_splits(m->max_seq, B, dm.Hk);
   Bufs bf;
   R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
@@ -365,8 +368,7 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
   if (!use_graph) {
     for (int64_t t = 0; t < num_tokens; ++t) {
       const int64_t pos = start_pos + t;
-      R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, attn_num_splits(pos + 1, B, dm.Hk), bf,
-                           true, st));
+      R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, true, st));
       R4Q_TRY(enqueue_sample(m, dm, B, bf, toks, false, (int)t, st));
     }
     return R4Q_OK;
@@ -427,7 +429,7 @@ extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* 
   Dims dm;
   R4Q_TRY(validate(m, 1, dm));
   R4Q_TRY(check_positions(m, pos, 1));
-  const int nsplit = attn_num_splits(pos + 1, 1, dm.Hk);
+  const int nsplit = attn_num_splits(m->max_seq, 1, dm.Hk);
   Bufs bf;
   R4Q_TRY(reserve(ctx, m, dm, 1, nsplit, bf));
   hipStream_t st = as_stream(stream);
