@@ -122,6 +122,19 @@ def gemv_roofline(dev, iters=200, copies=8):
     return us, alg
 
 
+def copy_calibration(dev, mib=256, iters=20):
+    """A plain copy of known size (fp16 negation: `mib` MiB read, `mib` MiB
+    written per launch) whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+    GEMV's counter readings to HBM bytes."""
+    import torch
+    src = torch.randn(mib * (1 << 20) // 2, device=dev, dtype=torch.float16)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    return mib * (1 << 20)
+
+
 def cpu_baseline(m, ctx):
     """Oracle (numpy) time per token on the host, from one full-width layer at
     `ctx` plus the LM head, extrapolated to all layers."""
@@ -173,6 +186,9 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline GEMV loop and the copy calibration "
+                         "(the program the counter runs profile)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -183,6 +199,13 @@ def main():
 
     import int4_hip
     dev = torch.device("cuda:0")
+    if args.roofline_only:
+        us, alg = gemv_roofline(dev)
+        nbytes = copy_calibration(dev)
+        print(json.dumps({"gemv_avg_us": round(us, 3), "gemv_alg_bytes": alg,
+                          "gemv_gbps": round(alg / us / 1e3, 1), "copy_bytes": nbytes}),
+              flush=True)
+        return
     log("building synthetic model")
     t0 = time.time()
     m = build_model(args.ctx, args.warmup + args.steps + 8, args.batch, dev)

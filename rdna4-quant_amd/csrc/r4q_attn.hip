@@ -56,7 +56,7 @@ template <int G>
 __global__ __launch_bounds__(256) void attn_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
-    float* __restrict__ part, int* __restrict__ counters, uint16_t* __restrict__ outp,
+    float* __restrict__ part, uint16_t* __restrict__ outp,
     int64_t out_stride, int fwht, int H, int Hk, int max_seq, int L_host,
     const int* __restrict__ L_dev, int nsplit) {
   const int sp = blockIdx.x, kh = blockIdx.y;
@@ -230,103 +230,110 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     for (int j = 0; j < 4; ++j) red[2 * wave + half][d4][4 * g + j] = o[g][j];
   __syncthreads();
 
+  // ---- reduce over the 8 (wave, half) slots into ostage[G][128]
+  float* ostage = &sc[0][0];
   const float oscale = vs * 256.0f;
-  float* out = part + ((b * H + (int64_t)kh * G) * nsplit + sp) * kPart;
   for (int e = t; e < G * 128; e += 256) {
     const int g = e >> 7, d = e & 127;
     float s = 0.f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) s += red[r][d >> 2][4 * g + (d & 3)];
-    out[(int64_t)g * nsplit * kPart + 4 + d] = s * oscale;
+    ostage[e] = s * oscale;
   }
-  if (t < G) {
-    out[(int64_t)t * nsplit * kPart + 0] = stat[t][0];
-    out[(int64_t)t * nsplit * kPart + 1] = stat[t][1];
-  }
+  __syncthreads();
 
-  // ---- the last workgroup to finish for this (sequence, kv head) merges the
-  // splits: m* = max m_s, out = sum e^(m_s-m*) o_s / sum e^(m_s-m*) l_s.
-  // The counter is reset by that workgroup, so it is zero between launches.
-  __shared__ int last;
-  __threadfence();  // publish this split's partials device-wide
-  __syncthreads();
-  if (t == 0) last = (atomicAdd(&counters[b * Hk + kh], 1) == nsplit - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // see every other split's partials
-  const float* pb = part + (b * H + (int64_t)kh * G) * nsplit * kPart;
-  float* wm = &sc[0][0];               // [G][nsplit] split maxima -> weights
-  float* wl = &sc[0][0] + G * nsplit;  // [G][nsplit] split sums
-  for (int e = t; e < G * nsplit; e += 256) {
-    wm[e] = pb[(int64_t)e * kPart];
-    wl[e] = pb[(int64_t)e * kPart + 1];
-  }
-  __syncthreads();
-  if (t < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, wm[t * nsplit + s]);
-    float Ls = 0.f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = wm[t * nsplit + s];
-      const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
-      wm[t * nsplit + s] = w;
-      Ls = __builtin_fmaf(w, wl[t * nsplit + s], Ls);
-    }
-    stat[t][1] = Ls;
-  }
-  __syncthreads();
-  float* ostage = &red[0][0][0];  // [G][128]
-  if (t < 32 * G) {
-    const int g = t >> 5, c4 = t & 31;
-    const float* po = pb + (int64_t)g * nsplit * kPart + 4 + 4 * c4;
-    f4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int s = 0; s < nsplit; ++s) {
-      const f4_t v = *reinterpret_cast<const f4_t*>(po + (int64_t)s * kPart);
-      const float w = wm[g * nsplit + s];
-      acc[0] = __builtin_fmaf(w, v[0], acc[0]);
-      acc[1] = __builtin_fmaf(w, v[1], acc[1]);
-      acc[2] = __builtin_fmaf(w, v[2], acc[2]);
-      acc[3] = __builtin_fmaf(w, v[3], acc[3]);
-    }
-    const float Ls = stat[g][1];
-    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ostage[g * 128 + 4 * c4 + j] = acc[j] * inv;
-  }
-  __syncthreads();
+  // ---- one thread per 32-dim chunk: FWHT-32 in registers (it is linear,
+  // so it commutes with the split merge), then either the final fp16 output
+  // (single split) or the fp32 partial (m, l, o).
   if (t < 4 * G) {
     const int g = t >> 2, c = t & 3;
     float v[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = ostage[g * 128 + 32 * c + i];
+    for (int i = 0; i < 32; i += 4) {
+      const f4_t x = *reinterpret_cast<const f4_t*>(&ostage[g * 128 + 32 * c + i]);
+      v[i] = x[0];
+      v[i + 1] = x[1];
+      v[i + 2] = x[2];
+      v[i + 3] = x[3];
+    }
     if (fwht) fwht32(v);
-    uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + g) * 128 + 32 * c;
+    if (nsplit == 1) {
+      const float l = stat[g][1];
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + g) * 128 + 32 * c;
 #pragma unroll
-    for (int i = 0; i < 32; i += 2)
-      *reinterpret_cast<uint32_t*>(dst + i) = (uint32_t)f2h(v[i]) | ((uint32_t)f2h(v[i + 1]) << 16);
+      for (int i = 0; i < 32; i += 8) {
+        u4_t w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = (uint32_t)f2h(v[i + 2 * j] * inv) | ((uint32_t)f2h(v[i + 2 * j + 1] * inv) << 16);
+        *reinterpret_cast<u4_t*>(dst + i) = w;
+      }
+    } else {
+      float* dst = part + ((b * H + (int64_t)kh * G + g) * nsplit + sp) * kPart;
+#pragma unroll
+      for (int i = 0; i < 32; i += 4) {
+        const f4_t x = {v[i], v[i + 1], v[i + 2], v[i + 3]};
+        *reinterpret_cast<f4_t*>(dst + 4 + 32 * c + i) = x;
+      }
+      if (c == 0) {
+        dst[0] = stat[g][0];
+        dst[1] = stat[g][1];
+      }
+    }
   }
-  if (t == 0) counters[b * Hk + kh] = 0;
+}
+
+// Split merge, one wave per (query head, sequence); lane j owns dims 2j and
+// 2j+1.  Every load is issued before any arithmetic:
+//   m* = max_s m_s,  out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s.
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part,
+                                                        uint16_t* __restrict__ outp,
+                                                        int64_t out_stride, int H, int nsplit) {
+  const int h = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
+  float ms = -INFINITY, ls = 0.f;
+  if (lane < nsplit) {
+    ms = pb[(int64_t)lane * kPart];
+    ls = pb[(int64_t)lane * kPart + 1];
+  }
+  float2 ov[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s)
+    if (s < nsplit) ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)s * kPart + 4 + 2 * lane);
+  const float M = wave_max(ms);
+  const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+  const float Ls = wave_sum(w * ls);
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    if (s < nsplit) {
+      const float ws = readlane_f(w, s);
+      a0 = __builtin_fmaf(ws, ov[s].x, a0);
+      a1 = __builtin_fmaf(ws, ov[s].y, a1);
+    }
+  }
+  const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+  *reinterpret_cast<uint32_t*>(outp + b * out_stride + (int64_t)h * 128 + 2 * lane) =
+      (uint32_t)f2h(a0 * inv) | ((uint32_t)f2h(a1 * inv) << 16);
 }
 
 }  // namespace
 
 int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
-  // One split per 64 positions of the cache, no more than ~4 workgroups
-  // per CU overall and at most kMaxSplits (the merge cost).  Depends only on
-  // the cache capacity, so a captured graph stays valid as the sequence grows.
-  const int64_t by_len = (cap_len + 63) / 64;
-  const int64_t by_chip = (1024 + B * Hk - 1) / (B * Hk);
-  int64_t n = by_len < by_chip ? by_len : by_chip;
+  // One split per 256-position tile of the cache (a workgroup costs about
+  // one memory latency per tile), at least ~256 workgroups once the cache
+  // is long enough to need them, at most kMaxSplits.  Depends only on the
+  // cache capacity, so a captured graph stays valid as the sequence grows.
+  int64_t n = (cap_len + kTile - 1) / kTile;
   if (n > kMaxSplits) n = kMaxSplits;
   return (int)(n < 1 ? 1 : n);
 }
 
-// Workspace: per-(sequence, kv head) arrival counters, then the partials.
-constexpr size_t kCounterBytes = 64 * 1024;
-
 size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit) {
-  return kCounterBytes + (size_t)B * H * nsplit * kPart * sizeof(float);
+  return nsplit > 1 ? (size_t)B * H * nsplit * kPart * sizeof(float) : 0;
 }
 
 int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, const void* v_cache,
@@ -334,19 +341,18 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
                         int64_t B, int64_t H, int64_t Hk, int64_t max_seq, int64_t seq_len,
                         const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st) {
   const int G = (int)(H / Hk);
-  if (nsplit < 1 || nsplit > kMaxSplits || B * Hk * 4 > (int64_t)kCounterBytes)
-    return fail(R4Q_EUNSUPPORTED, "flash_decode: %d splits / %lld heads exceed the workspace",
-                nsplit, (long long)(B * Hk));
+  if (nsplit < 1 || nsplit > kMaxSplits)
+    return fail(R4Q_EUNSUPPORTED, "flash_decode: %d splits outside [1, %d]", nsplit, kMaxSplits);
+  if (nsplit > 1 && !ws) return fail(R4Q_EINVAL, "flash_decode: no split workspace");
   const dim3 grid((unsigned)nsplit, (unsigned)Hk, (unsigned)B);
-  int* counters = reinterpret_cast<int*>(ws);
-  float* part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + kCounterBytes);
+  float* part = ws;
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
   const auto* vp = static_cast<const uint8_t*>(v_cache);
 #define R4Q_ATTN(GG)                                                                        \
   case GG:                                                                                  \
     hipLaunchKernelGGL((attn_partial_kernel<GG>), grid, dim3(256), 0, st, qp, q_stride, kp, vp, \
-                       k_scale, v_scale, part, counters, static_cast<uint16_t*>(out), out_stride, \
+                       k_scale, v_scale, part, static_cast<uint16_t*>(out), out_stride,           \
                        fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len, seq_len_dev, nsplit); \
     break;
   switch (G) {
@@ -359,6 +365,9 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
       return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
   }
 #undef R4Q_ATTN
+  if (nsplit > 1)
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)H, (unsigned)B), dim3(64), 0, st, part,
+                       static_cast<uint16_t*>(out), out_stride, (int)H, nsplit);
   return launch_status("flash_decode");
 }
 
@@ -374,9 +383,6 @@ int DevBuf::reserve(size_t need) {
     ptr = nullptr;
     return fail(R4Q_ENOMEM, "hipMalloc(%zu) failed", cap);
   }
-  // zeroed once: the attention arrival counters rely on it (they are reset
-  // to zero by the kernel that consumes them)
-  if (hipMemset(ptr, 0, cap) != hipSuccess) return fail(R4Q_EHIP, "hipMemset failed");
   bytes = cap;
   return R4Q_OK;
 }
@@ -403,6 +409,7 @@ extern "C" int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
   R4Q_REQUIRE(q_stride >= H * D && (q_stride % 8) == 0 &&
                   (reinterpret_cast<uintptr_t>(q) & 15) == 0,
               "flash_decode: q rows must be 16-byte aligned with stride >= H*D");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15) == 0, "flash_decode: out must be 16-byte aligned");
   const int nsplit = r4q::attn_num_splits(seq_len, B, Hk);
   R4Q_TRY(ctx->attn.reserve(r4q::attn_ws_bytes(B, H, nsplit)));
   return r4q::launch_flash_decode(q, q_stride, k_cache, v_cache, k_scale, v_scale, out, H * D, B,
