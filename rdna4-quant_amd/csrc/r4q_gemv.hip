@@ -6,9 +6,9 @@
 //
 // gfx950 design
 //  * A "chunk" is 16 bytes of one weight row (INT4: one 32-element block,
-//    INT8: half a block, FP16: 8 values).  The chunks of a row are spread over
-//    LR = gcd(chunks_per_row, 64) lanes, so a wave covers 64/LR rows per step
-//    and every wave-level dwordx4 load reads contiguous 512-1024 B runs.
+//    INT8: half a block, FP16: 8 values).  LPR lanes share a row (16..64
+//    inside a wave, 128/256 over 2/4 waves) and lane c owns chunk columns
+//    c + LPR*i, so every wave-level dwordx4 load reads contiguous runs.
 //  * Weights are streamed with nontemporal 128-bit loads (read once).
 //  * Nibbles become fp16 without per-element converts: (w & 0x000F000F) |
 //    0x64006400 is the fp16 pair (1024+q0, 1024+q4); the 0x00F000F0 mask gives
@@ -18,11 +18,13 @@
 //      sum x*(q-zp) = A + B/16 - (1024*S_even + 64*S_odd) - zp*(S_even+S_odd)
 //    where A/B are the even/odd-element dot accumulators.  INT8 bytes use
 //    v_perm to form (1024+q) pairs the same way.
-//  * The activation is arranged once per workgroup into LDS in that pair
-//    order, with the per-chunk sums; waves keep it in registers when a row is
-//    short (K=5120) and stream it from LDS otherwise (K=17408).
-//  * Row partials are reduced across the LR lanes with DPP row operations and
-//    v_readlane; no LDS round trip.
+//  * The first batch of weight loads is issued before the activation is
+//    arranged (once per workgroup, in LDS, in that pair order with the
+//    per-chunk sums) and copied into registers; later batches are
+//    double-buffered in registers, one batch ahead of the arithmetic.
+//  * Row partials are reduced across lanes with DPP row operations and
+//    v_readlane; rows spread over waves combine per-wave partials through
+//    LDS once, at the end of the workgroup.
 #include <stdlib.h>
 
 #include "r4q_device.hpp"
@@ -38,16 +40,19 @@ template <>
 struct Fmt<4> {
   static constexpr int kElems = 32;  // elements per 16-byte chunk
   static constexpr int kXDw = 20;    // prepared-x dwords per chunk
+  static constexpr int kCpl = 5;     // chunk columns per lane (x in VGPRs)
 };
 template <>
 struct Fmt<8> {
   static constexpr int kElems = 16;
   static constexpr int kXDw = 12;
+  static constexpr int kCpl = 5;
 };
 template <>
 struct Fmt<16> {
   static constexpr int kElems = 8;
   static constexpr int kXDw = 4;
+  static constexpr int kCpl = 10;
 };
 
 constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
@@ -206,117 +211,124 @@ __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, i
   else return 0u;
 }
 
-// Register-resident activation: each lane owns exactly CPL chunk columns
-// (cpr == CPL * lr), holds their prepared x in VGPRs and sweeps rows.
-template <int WBITS, int CPL>
-__global__ __launch_bounds__(256) void gemv_xreg_kernel(const uint16_t* __restrict__ x,
-                                                        const uint8_t* __restrict__ w,
-                                                        const uint32_t* __restrict__ sz,
-                                                        uint16_t* __restrict__ y, int N, int K,
-                                                        int lr, int upw) {
-  constexpr int E = Fmt<WBITS>::kElems;
-  constexpr int XD = Fmt<WBITS>::kXDw;
-  extern __shared__ __align__(16) uint32_t xs[];
-  const int cpr = K / E;
-  const int nb = K / 32;
-  stage_x<WBITS>(x, xs, cpr);
+// Rows are processed in "steps" of RPS = 256/LPR rows per workgroup: LPR
+// lanes share a row (LPR <= 64: inside one wave; 128/256: 2/4 waves) and
+// lane `cl` of a row owns chunk columns cl + LPR*i, i < CPL (columns past the
+// row end are masked).  Workgroup g takes steps g, g + grid, ...; UB steps
+// form a batch and the next batch's weight loads are issued before the
+// current batch is computed (two register buffers).  The first batch is
+// requested before the activation is staged, so that staging hides behind
+// the weight stream.
+template <int WBITS, int LPR, int CPL, int UB>
+struct GemvTile {
+  static constexpr int RPS = 256 / LPR;
+  u4_t wq[UB][CPL];
+  uint32_t s2[UB][CPL];
+};
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rpu = 64 / lr;
-  const int rl = lane / lr;
-  const int cl = lane % lr;
-  uint32_t xr[CPL * XD];
+template <int WBITS, int LPR, int CPL, int UB>
+__device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
+                                          const uint8_t* __restrict__ w,
+                                          const uint32_t* __restrict__ sz, int64_t row_bytes,
+                                          int nb, int cpr, int N, int step0, int stride,
+                                          int nsteps, int rs, int cl) {
+  constexpr int RPS = 256 / LPR;
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) lds_copy<XD>(xs + (cl + lr * i) * XD, xr + i * XD);
-
-  const int64_t row_bytes = (int64_t)K * WBITS / 8;
-  const int units = (N + rpu - 1) / rpu;
-  const int u0 = (blockIdx.x * (blockDim.x >> 6) + wave) * upw;
-  const int u1 = min(u0 + upw, units);
-  for (int u = u0; u < u1; ++u) {
-    const int row = u * rpu + rl;
-    const int rowc = min(row, N - 1);  // clamped: loads stay in bounds
-    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes) + cl;
+  for (int j = 0; j < UB; ++j) {
+    const int step = min(step0 + j * stride, nsteps - 1);  // clamped: in bounds
+    const int rowc = min(step * RPS + rs, N - 1);
+    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes);
     const uint32_t* srow = sz + (int64_t)rowc * nb;
-    u4_t wq[CPL];
-    uint32_t s2[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      wq[i] = load_nt(wrow + lr * i);
-      s2[i] = load_sz<WBITS>(srow, cl + lr * i);
+      const int c = min(cl + LPR * i, cpr - 1);
+      t.wq[j][i] = load_nt(wrow + c);
+      t.s2[j][i] = load_sz<WBITS>(srow, c);
     }
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) acc = chunk_dot<WBITS>(wq[i], s2[i], xr + i * XD, acc);
-    const float total = reduce_lr(acc, lr);
-    if (row < N && cl == 0) y[row] = f2h(total);
   }
 }
 
-// LDS-resident activation for long rows: batches of NB chunk slots, the
-// prepared x of each chunk read from LDS as it is consumed.
-template <int WBITS, int NB>
-__global__ __launch_bounds__(256) void gemv_stream_kernel(const uint16_t* __restrict__ x,
-                                                          const uint8_t* __restrict__ w,
-                                                          const uint32_t* __restrict__ sz,
-                                                          uint16_t* __restrict__ y, int N,
-                                                          int K, int lr, int upw) {
-  constexpr int E = Fmt<WBITS>::kElems;
+// Computes the UB steps of a batch.  Rows spread over several waves leave
+// one partial per (step, wave) in `red` (indexed by the step's ordinal k in
+// this workgroup); they are combined once, after the last batch.
+template <int WBITS, int LPR, int CPL, int UB>
+__device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>& t,
+                                             const uint32_t* __restrict__ xr,
+                                             uint16_t* __restrict__ y, float* red, int cpr,
+                                             int N, int step0, int k0, int stride, int nsteps,
+                                             int rs, int cl) {
   constexpr int XD = Fmt<WBITS>::kXDw;
-  extern __shared__ __align__(16) uint32_t xs[];
-  const int cpr = K / E;
-  const int cpl = cpr / lr;
-  const int nb = K / 32;
-  stage_x<WBITS>(x, xs, cpr);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rpu = 64 / lr;
-  const int rl = lane / lr;
-  const int cl = lane % lr;
-
-  const int64_t row_bytes = (int64_t)K * WBITS / 8;
-  const int units = (N + rpu - 1) / rpu;
-  const int u0 = (blockIdx.x * (blockDim.x >> 6) + wave) * upw;
-  const int u1 = min(u0 + upw, units);
-  for (int u = u0; u < u1; ++u) {
-    const int row = u * rpu + rl;
-    const int rowc = min(row, N - 1);
-    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes) + cl;
-    const uint32_t* srow = sz + (int64_t)rowc * nb;
+  constexpr int RPS = 256 / LPR;
+#pragma unroll
+  for (int j = 0; j < UB; ++j) {
+    const int step = step0 + j * stride;
+    if (step >= nsteps) break;  // workgroup-uniform
     float acc = 0.f;
-    for (int i0 = 0; i0 < cpl; i0 += NB) {
-      const int nslot = min(NB, cpl - i0);  // wave-uniform
-      u4_t wq[NB];
-      uint32_t s2[NB];
 #pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        const int slot = i0 + min(i, nslot - 1);  // clamped: always in bounds
-        wq[i] = load_nt(wrow + lr * slot);
-        s2[i] = load_sz<WBITS>(srow, cl + lr * slot);
-      }
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        if (i < nslot) {
-          uint32_t xp[XD];
-          lds_copy<XD>(xs + (cl + lr * (i0 + i)) * XD, xp);
-          acc = chunk_dot<WBITS>(wq[i], s2[i], xp, acc);
-        }
-      }
+    for (int i = 0; i < CPL; ++i) {
+      if (LPR * CPL <= cpr || cl + LPR * i < cpr)
+        acc = chunk_dot<WBITS>(t.wq[j][i], t.s2[j][i], xr + i * XD, acc);
     }
-    const float total = reduce_lr(acc, lr);
-    if (row < N && cl == 0) y[row] = f2h(total);
+    if constexpr (LPR <= 64) {
+      const int row = step * RPS + rs;
+      const float total = reduce_lr(acc, LPR);
+      if (row < N && cl == 0) y[row] = f2h(total);
+    } else {
+      const float total = reduce_lr(acc, 64);
+      if ((threadIdx.x & 63) == 0) red[(k0 + j) * 4 + (threadIdx.x >> 6)] = total;
+    }
   }
 }
 
-int gcd_int(int a, int b) {
-  while (b) {
-    const int t = a % b;
-    a = b;
-    b = t;
+template <int WBITS, int LPR, int CPL, int UB>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x,
+                                                   const uint8_t* __restrict__ w,
+                                                   const uint32_t* __restrict__ sz,
+                                                   uint16_t* __restrict__ y, int N, int K) {
+  constexpr int XD = Fmt<WBITS>::kXDw;
+  constexpr int RPS = 256 / LPR;
+  constexpr int WPR = LPR > 64 ? LPR / 64 : 1;  // waves per row
+  extern __shared__ __align__(16) uint32_t xs[];
+  const int cpr = K / Fmt<WBITS>::kElems;
+  const int nb = K / 32;
+  const int64_t row_bytes = (int64_t)K * WBITS / 8;
+  const int nsteps = (N + RPS - 1) / RPS;
+  const int rs = threadIdx.x / LPR, cl = threadIdx.x % LPR;
+  const int g = blockIdx.x, G = gridDim.x;
+
+  GemvTile<WBITS, LPR, CPL, UB> ta, tb;
+  gemv_load(ta, w, sz, row_bytes, nb, cpr, N, g, G, nsteps, rs, cl);
+
+  stage_x<WBITS>(x, xs, cpr);
+  uint32_t xr[CPL * XD];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) lds_copy<XD>(xs + min(cl + LPR * i, cpr - 1) * XD, xr + i * XD);
+  // the staging area becomes the cross-wave partial buffer
+  float* red = reinterpret_cast<float*>(xs);
+  if constexpr (WPR > 1) __syncthreads();
+
+  const int batch = UB * G;
+  int k = 0;
+  for (int s0 = g; s0 < nsteps; s0 += 2 * batch, k += 2 * UB) {
+    if (s0 + batch < nsteps)
+      gemv_load(tb, w, sz, row_bytes, nb, cpr, N, s0 + batch, G, nsteps, rs, cl);
+    gemv_compute(ta, xr, y, red, cpr, N, s0, k, G, nsteps, rs, cl);
+    if (s0 + 2 * batch < nsteps)
+      gemv_load(ta, w, sz, row_bytes, nb, cpr, N, s0 + 2 * batch, G, nsteps, rs, cl);
+    if (s0 + batch < nsteps)
+      gemv_compute(tb, xr, y, red, cpr, N, s0 + batch, k + UB, G, nsteps, rs, cl);
   }
-  return a;
+  if constexpr (WPR > 1) {
+    __syncthreads();
+    const int nlocal = (nsteps - g + G - 1) / G;
+    for (int e = threadIdx.x; e < nlocal * RPS; e += 256) {
+      const int kk = e / RPS, r = e % RPS;
+      const int row = (g + kk * G) * RPS + r;
+      const float* p = red + kk * 4 + r * WPR;
+      const float total = WPR == 2 ? p[0] + p[1] : (p[0] + p[1]) + (p[2] + p[3]);
+      if (row < N) y[row] = f2h(total);
+    }
+  }
 }
 
 int env_int(const char* name, int dflt) {
@@ -330,49 +342,44 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
                     hipStream_t st) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
+  constexpr int kCpl = Fmt<WBITS>::kCpl;
   const int cpr = (int)(K / E);
-  const int lr = gcd_int(cpr, 64);
-  const int cpl = cpr / lr;
-  const int rpu = 64 / lr;
-  const int64_t units = (N + rpu - 1) / rpu;
   const size_t lds = (size_t)cpr * XD * 4;
   R4Q_REQUIRE(lds <= 64 * 1024, "gemv: K=%lld too large for the LDS activation stage",
               (long long)K);
-  // Units per wave: aim at ~2048 waves over the chip (256 CUs x 8).
-  static const int target_waves = env_int("R4Q_GEMV_WAVES", 2048);
-  int upw = (int)((units + target_waves - 1) / target_waves);
-  if (upw < 1) upw = 1;
-  const int64_t waves = (units + upw - 1) / upw;
-  const int64_t grid = (waves + 3) / 4;
-  const dim3 g((unsigned)grid), b(256);
+  // lanes per row: the fewest (>= 16) that keep every lane at <= 5 chunks,
+  // or at <= kCpl when 256 lanes cannot
+  int lpr = 16;
+  while (lpr < 256 && lpr * 5 < cpr) lpr *= 2;
+  lpr = env_int("R4Q_GEMV_LPR", lpr);
+  R4Q_REQUIRE(lpr * kCpl >= cpr, "gemv: K=%lld needs more than 256 lanes per row", (long long)K);
+  const int rps = 256 / lpr;
+  const int64_t nsteps = (N + rps - 1) / rps;
+  // Workgroups: about the resident capacity (measured best: 4 per CU for
+  // rows inside one wave, 2-3 per CU for rows spread over waves), with an
+  // equal number of steps each.
+  const int max_wg = env_int("R4Q_GEMV_WGS", lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
+  const int ub = env_int("R4Q_GEMV_UB", 1);
+  const int64_t per = (nsteps + max_wg - 1) / max_wg;
+  const int64_t grid = (nsteps + per - 1) / per;
+  // the staging area also holds one partial per (step, wave) of the workgroup
+  const size_t lds_all = lds > (size_t)per * 16 ? lds : (size_t)per * 16;
+  R4Q_REQUIRE(lds_all <= 64 * 1024, "gemv: N=%lld too large for one launch", (long long)N);
+  const dim3 gd((unsigned)grid), bd(256);
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
-#define R4Q_XREG(C)                                                                       \
-  case C:                                                                                 \
-    hipLaunchKernelGGL((gemv_xreg_kernel<WBITS, C>), g, b, lds, st, xp, wp, sp, yp, (int)N, \
-                       (int)K, lr, upw);                                                  \
-    break;
-  switch (cpl) {
-    R4Q_XREG(1)
-    R4Q_XREG(2)
-    R4Q_XREG(3)
-    R4Q_XREG(4)
-    R4Q_XREG(5)
-    default:
-      if constexpr (WBITS == 16) {
-        if (cpl == 10) {
-          hipLaunchKernelGGL((gemv_xreg_kernel<WBITS, 10>), g, b, lds, st, xp, wp, sp, yp,
-                             (int)N, (int)K, lr, upw);
-          break;
-        }
-      }
-      hipLaunchKernelGGL((gemv_stream_kernel<WBITS, 9>), g, b, lds, st, xp, wp, sp, yp, (int)N,
-                         (int)K, lr, upw);
+#define R4Q_GEMV(L, U)                                                                     \
+  if (lpr == L && ub == U) {                                                               \
+    hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U>), gd, bd, lds_all, st, xp, wp, sp, yp, \
+                       (int)N, (int)K);                                                    \
+    return launch_status("gemv");                                                          \
   }
-#undef R4Q_XREG
-  return launch_status("gemv");
+  R4Q_GEMV(16, 1) R4Q_GEMV(32, 1) R4Q_GEMV(64, 1) R4Q_GEMV(128, 1) R4Q_GEMV(256, 1)
+  R4Q_GEMV(16, 2) R4Q_GEMV(32, 2) R4Q_GEMV(64, 2) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
+#undef R4Q_GEMV
+  return fail(R4Q_EUNSUPPORTED, "gemv: no kernel for %d lanes/row, %d steps/batch", lpr, ub);
 }
 
 }  // namespace
