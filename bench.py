@@ -33,6 +33,25 @@ sys.path.insert(0, PKG)
 
 METRIC = "INT4 GEMV HBM GB/s (% of peak); decode tok/s at ctx=2048, batch 1"
 HBM_PEAK_GBPS = 8000.0
+ROOFLINE_KERNEL = "gemv_kernel<4, 32, 5, 1>"
+# Counter-derived HBM bytes per launch of ROOFLINE_KERNEL (FETCH_SIZE + WRITE_SIZE
+# passes, calibrated against a copy of known size), written by that measurement.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int4_gemv_5120x17408_roofline.md")
+
+
+def measured_traffic():
+    """traffic_bytes_per_launch from the counter summary, if it covers the
+    kernel this build launches; None otherwise."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    if ROOFLINE_KERNEL not in text:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def log(msg):
@@ -96,28 +115,51 @@ def bench_args(m, start_pos):
             m["lm_w"], None, m["V"], m["D"], had)
 
 
-def gemv_roofline(dev, iters=200, copies=8):
-    """Average duration of the config-0 INT4 GEMV and its algorithmic GB/s."""
+def gemv_roofline(dev, iters=200, copies=8, eager_tail=0):
+    """Average duration of the config-0 INT4 GEMV and its algorithmic bytes.
+
+    `iters` launches through the C ABI (cycling `copies` weight sets, more
+    than the 256 MB last-level cache holds) are captured into one hipGraph on
+    a private stream and replayed; HIP events on that same stream bracket the
+    replays, so the figure is GPU time, not Python launch rate."""
     import torch
 
-    import int4_hip
+    import r4q_lib as R
     import r4q_synth as S
     N, K = 17408, 5120
     g = S.gen(0, dev)
     ws = [S.int4_weight(N, K, g, dev) for _ in range(copies)]
     x = S.rotated_activation(K, g, dev)[0]
-    for w, s in ws:
-        int4_hip.dbg_gemv(x, w, s, N, K)
+    y = torch.empty(N, dtype=torch.float16, device=dev)
+    st = torch.cuda.Stream(dev)
+
+    def launch(i):
+        w, s = ws[i % copies]
+        R.call("r4q_gemv", x.data_ptr(), w.data_ptr(), s.data_ptr(), y.data_ptr(), N, K, 4,
+               st.cuda_stream)
+
+    for i in range(copies):
+        launch(i)
     torch.cuda.synchronize()
-    st = torch.cuda.current_stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        for i in range(iters):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = 5
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
-    for i in range(iters):
-        w, s = ws[i % copies]
-        int4_hip.dbg_gemv(x, w, s, N, K)
+    with torch.cuda.stream(st):
+        for _ in range(reps):
+            graph.replay()
     e1.record(st)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / iters
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+    # eager launches for per-dispatch counter collection
+    for i in range(eager_tail):
+        launch(i)
+    torch.cuda.synchronize()
     alg = N * K // 2 + N * (K // 32) * 3 + 2 * K + 2 * N
     return us, alg
 
@@ -200,7 +242,7 @@ def main():
     import int4_hip
     dev = torch.device("cuda:0")
     if args.roofline_only:
-        us, alg = gemv_roofline(dev)
+        us, alg = gemv_roofline(dev, eager_tail=2 * 8)
         nbytes = copy_calibration(dev)
         print(json.dumps({"gemv_avg_us": round(us, 3), "gemv_alg_bytes": alg,
                           "gemv_gbps": round(alg / us / 1e3, 1), "copy_bytes": nbytes}),
@@ -264,13 +306,13 @@ def main():
         "step_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "int4_gemv_gbps": round(gbps, 1),
         "roofline": {
-            "kernel": "INT4 GEMV K=5120 -> N=17408 (gemv_xreg_kernel<4,5>)",
+            "kernel": f"INT4 GEMV K=5120 -> N=17408 ({ROOFLINE_KERNEL})",
             "bound": "hbm",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_us": round(us, 3),
             "bytes_per_launch": alg,
         },

@@ -40,9 +40,9 @@
  *   r4q_head_norm_rope_kv<- head_rmsnorm_rope_kv    (:1620-1683)
  *   r4q_flash_decode     <- launch_flash_decode     (:1547-1593)
  *   r4q_decode_step      <- decode_step / decode_step_logits (:2343-2595)
- *   r4q_decode_bench     <- decode_bench / decode_bench_graph (:2601-3041)
+ *   r4q_decode_bench     <- decode_bench / decode_bench_graph (:2601-3041),
+ *                           and decode_loop (:3284-3466) via tokens_out
  *   r4q_decode_profile   <- decode_profile          (:3047-3273)
- *   r4q_decode_loop      <- decode_loop             (:3284-3466)
  *   r4q_prefill_logits   <- prefill_logits          (:2127-2320)
  */
 #ifndef R4Q_H

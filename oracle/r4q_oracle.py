@@ -29,8 +29,10 @@ PINNING = {
     "dequant_int4/dequant_int8": "exhaustive closed form over q, zp and every finite fp16 "
                                  "scale (float64 route) + reference test "
                                  "(tests/test_kernels.py:53-70)",
-    "fp8_encode": "all 63488 finite fp16 inputs vs torch.float8_e4m3fn with every "
-                  "difference classified (flush / tie / saturation) and counted",
+    "fp8_encode": "all 65536 fp16 inputs vs the golden table derived with exact "
+                  "rationals (tests/golden/make_fp8_table.py); all 63488 finite fp16 "
+                  "inputs vs torch.float8_e4m3fn with every difference classified "
+                  "(flush / tie / saturation) and counted",
     "fp8_decode": "all 256 codes vs torch.float8_e4m3fn values",
     "fwht32": "Sylvester matrix (hadamard_utils.py:14-34), H H = I "
               "(tests/test_kernels.py:73-79), unit vectors, float64 matrix product",

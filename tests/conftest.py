@@ -26,6 +26,16 @@ def pytest_collection_modifyitems(config, items):
             it.add_marker(skip)
 
 
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def fp8_golden_table():
+    """E4M3 code of every fp16 bit pattern, derived in the value domain with
+    exact rationals (tests/golden/make_fp8_table.py)."""
+    import numpy as np
+    return np.fromfile(GOLDEN / "fp8_e4m3_from_fp16.bin", dtype=np.uint8)
+
+
 def rel_l2(a, b):
     """||a - b|| / ||b|| in float64 (numpy or torch inputs)."""
     import numpy as np

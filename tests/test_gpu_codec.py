@@ -6,6 +6,7 @@ import torch
 import int4_hip
 import r4q_oracle as O
 import r4q_synth as S
+from conftest import fp8_golden_table
 
 pytestmark = pytest.mark.gpu
 
@@ -16,6 +17,7 @@ def test_fp16_to_fp8_all_bit_patterns(dev):
     got = int4_hip.fp16_to_fp8(x).cpu().numpy()
     want = O.fp8_encode(bits.view(np.float16).astype(np.float32))
     assert np.array_equal(got, want)
+    assert np.array_equal(got, fp8_golden_table())
 
 
 @pytest.mark.parametrize("n", [1, 3, 4, 5, 1000003])

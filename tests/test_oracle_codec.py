@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import r4q_oracle as O
+from conftest import fp8_golden_table
 
 pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
 
@@ -144,6 +145,17 @@ def test_fp8_encode_all_fp16_vs_torch_classified():
     # exact ties, resolved away from zero instead of to even
     assert np.allclose(np.abs(x[ties] - tv), np.abs(ov - x[ties]), rtol=0, atol=0)
     assert np.all(np.abs(ov) > np.abs(tv))
+
+
+def test_fp8_encode_all_fp16_vs_golden_table():
+    """Golden fixture: value-domain derivation (exact rationals, ties away from
+    zero, flush/saturate rules) of the reference encoder for all 65,536 fp16
+    inputs; the oracle's bit recipe must agree on every code."""
+    table = fp8_golden_table()
+    assert table.size == 65536
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.fp8_encode(bits.view(np.float16).astype(np.float32))
+    assert np.array_equal(got, table)
 
 
 def test_fp8_encode_special_values():
