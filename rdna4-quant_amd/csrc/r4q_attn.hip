@@ -39,7 +39,7 @@
 namespace r4q {
 namespace {
 
-constexpr int kTile = 256;       // positions per tile (scores staged in LDS)
+constexpr int kMaxTile = 256;    // longest tile (positions whose scores sit in LDS)
 constexpr int kMaxSplits = 64;   // partials merged by the last workgroup
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 
@@ -52,7 +52,7 @@ __device__ __forceinline__ void fp8x4_to_h2_div256(uint32_t w, uint32_t& h02, ui
   h13 = (w & m1) | ((w >> 1) & m2);
 }
 
-template <int G>
+template <int G, int TILE>
 __global__ __launch_bounds__(256) void attn_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
@@ -67,8 +67,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
   const int n = max(0, min(L, s0 + S) - s0);
 
   // 128-bit LDS accesses below need 16-byte aligned rows
-  __shared__ __align__(16) float sc[G][kTile];
-  __shared__ __align__(16) uint32_t pp[G][kTile / 2];
+  __shared__ __align__(16) float sc[G][TILE < 128 ? 128 : TILE];  // also the output stage
+  __shared__ __align__(16) uint32_t pp[G][TILE / 2];
   __shared__ __align__(16) float red[8][32][G * 4];
   __shared__ float stat[G][4];  // running max, running sum, tile rescale
 
@@ -79,50 +79,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
   const uint8_t* kbase = kc + head_off;
   const uint8_t* vbase = vc + head_off;
 
-  // ---- query pairs matching the K decode order
   const int dq = t & 3;
-  uint32_t qp[G][16];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride + (int64_t)(kh * G + g) * 128 +
-                                                   32 * dq);
-    uint32_t raw[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u4_t v = qr[i];
-      raw[4 * i] = v[0];
-      raw[4 * i + 1] = v[1];
-      raw[4 * i + 2] = v[2];
-      raw[4 * i + 3] = v[3];
-    }
-    // K dword j holds dims 4j..4j+3 -> pairs (4j, 4j+2), (4j+1, 4j+3)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t a = raw[2 * j], c = raw[2 * j + 1];
-      qp[g][2 * j] = (a & 0xFFFFu) | (c << 16);
-      qp[g][2 * j + 1] = (a >> 16) | (c & 0xFFFF0000u);
-    }
-  }
-  if (t < G) {
-    stat[t][0] = -INFINITY;
-    stat[t][1] = 0.f;
-  }
-
   const int d4 = lane & 31, half = lane >> 5;
-  float o[G][4];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[g][j] = 0.f;
 
-  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
-  for (int base = 0; base < n; base += kTile) {
-    const int nt = min(kTile, n - base);
-    // ---- issue every K and V load of the tile before any arithmetic, so a
-    // tile costs one memory latency.  Rows past the tile end are clamped to
-    // its last row; their scores become -inf and their probabilities 0.
-    constexpr int kPass = kTile / 64;
-    u4_t kw[kPass][2];
+  // ---- K and V loads of a tile.  Rows past the tile end are clamped to its
+  // last row; their scores become -inf and their probabilities 0.
+  constexpr int kPass = TILE / 64;   // 64 positions per QK pass
+  constexpr int kPairs = TILE / 16;  // position pairs per (wave, half) slot
+  u4_t kw[kPass][2];
+  uint32_t va[kPairs], vb[kPairs];
+  auto load_k = [&](int base, int nt) {
 #pragma unroll
     for (int pass = 0; pass < kPass; ++pass) {
       const int p = min(pass * 64 + (t >> 2), nt - 1);
@@ -130,8 +96,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
       kw[pass][0] = __builtin_nontemporal_load(kr);
       kw[pass][1] = __builtin_nontemporal_load(kr + 1);
     }
-    constexpr int kPairs = kTile / 16;  // pairs per (wave, half) slot
-    uint32_t va[kPairs], vb[kPairs];
+  };
+  auto load_v = [&](int base, int nt) {
 #pragma unroll
     for (int k = 0; k < kPairs; ++k) {
       const int i = 2 * wave + half + 8 * k;
@@ -141,7 +107,56 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
       vb[k] = __builtin_nontemporal_load(
           reinterpret_cast<const uint32_t*>(vbase + (int64_t)(base + r1) * 128 + 4 * d4));
     }
+  };
 
+  // ---- query rows first, then the first tile: both in flight together
+  uint32_t qraw[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride + (int64_t)(kh * G + g) * 128 +
+                                                   32 * dq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u4_t v = qr[i];
+      qraw[g][4 * i] = v[0];
+      qraw[g][4 * i + 1] = v[1];
+      qraw[g][4 * i + 2] = v[2];
+      qraw[g][4 * i + 3] = v[3];
+    }
+  }
+  if (n > 0) {
+    load_k(0, min(TILE, n));
+    load_v(0, min(TILE, n));
+  }
+
+  // ---- query pairs matching the K decode order:
+  // K dword j holds dims 4j..4j+3 -> pairs (4j, 4j+2), (4j+1, 4j+3)
+  uint32_t qp[G][16];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t a = qraw[g][2 * j], c = qraw[g][2 * j + 1];
+      qp[g][2 * j] = (a & 0xFFFFu) | (c << 16);
+      qp[g][2 * j + 1] = (a >> 16) | (c & 0xFFFF0000u);
+    }
+  }
+  if (t < G) {
+    stat[t][0] = -INFINITY;
+    stat[t][1] = 0.f;
+  }
+
+  float o[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[g][j] = 0.f;
+
+  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
+  for (int base = 0; base < n; base += TILE) {
+    const int nt = min(TILE, n - base);
+    // (this tile's K and V were requested before the previous tile's
+    // arithmetic, or before the query prep for the first tile)
     // ---- Q K^T, 4 lanes per position, 64 positions per pass
 #pragma unroll
     for (int pass = 0; pass < kPass; ++pass) {
@@ -172,22 +187,38 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
         for (int g = 0; g < G; ++g) sc[g][p] = (p < nt) ? acc[g] * sscale : -INFINITY;
       }
     }
+    const int nb = base + TILE;  // next tile
+    if (nb < n) load_k(nb, min(TILE, n - nb));
     __syncthreads();
 
     // ---- online softmax: tile max, rescale of the running state, fp16
-    // probabilities of position pairs
+    // probabilities of position pairs.  Lane j holds positions PPL*j ...
+    constexpr int PPL = TILE >= 256 ? 4 : 2;
+    const bool act = lane * PPL < TILE;
     for (int g = wave; g < G; g += 4) {
-      const f4_t v = *reinterpret_cast<const f4_t*>(&sc[g][4 * lane]);
-      const float mt = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+      float v[PPL];
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) v[i] = act ? sc[g][PPL * lane + i] : -INFINITY;
+      float vm = v[0];
+#pragma unroll
+      for (int i = 1; i < PPL; ++i) vm = fmaxf(vm, v[i]);
+      const float mt = wave_max(vm);
       const float mo = stat[g][0];
       const float mn = fmaxf(mo, mt);
       const float alpha = (mo == -INFINITY) ? 0.f : __expf(mo - mn);
-      float pr[4];
+      float pr[PPL], ps = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pr[i] = (mn == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - mn)));
-      const float l = wave_sum((pr[0] + pr[1]) + (pr[2] + pr[3]));
-      pp[g][2 * lane] = (uint32_t)f2h(pr[0]) | ((uint32_t)f2h(pr[1]) << 16);
-      pp[g][2 * lane + 1] = (uint32_t)f2h(pr[2]) | ((uint32_t)f2h(pr[3]) << 16);
+      for (int i = 0; i < PPL; ++i) {
+        pr[i] = (mn == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - mn)));
+        ps += pr[i];
+      }
+      const float l = wave_sum(ps);
+      if (act) {
+#pragma unroll
+        for (int j = 0; j < PPL / 2; ++j)
+          pp[g][(PPL / 2) * lane + j] =
+              (uint32_t)f2h(pr[2 * j]) | ((uint32_t)f2h(pr[2 * j + 1]) << 16);
+      }
       if (lane == 0) {
         stat[g][0] = mn;
         stat[g][1] = __builtin_fmaf(stat[g][1], alpha, l);
@@ -221,6 +252,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
         o[g][3] = __builtin_amdgcn_fdot2(as_h2(h3), pg, o[g][3], false);
       }
     }
+    if (nb < n) load_v(nb, min(TILE, n - nb));
     __syncthreads();  // sc / pp / stat rescale reused by the next tile
   }
 
@@ -323,11 +355,11 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
 }  // namespace
 
 int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
-  // One split per 256-position tile of the cache (a workgroup costs about
-  // one memory latency per tile), at least ~256 workgroups once the cache
-  // is long enough to need them, at most kMaxSplits.  Depends only on the
-  // cache capacity, so a captured graph stays valid as the sequence grows.
-  int64_t n = (cap_len + kTile - 1) / kTile;
+  // One split per 64 positions of the cache capacity, at most kMaxSplits
+  // (beyond that a workgroup walks several 256-position tiles).  Depends only
+  // on the cache capacity, so a captured graph stays valid as the sequence
+  // grows.
+  int64_t n = (cap_len + 63) / 64;
   if (n > kMaxSplits) n = kMaxSplits;
   return (int)(n < 1 ? 1 : n);
 }
@@ -349,21 +381,25 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
   const auto* vp = static_cast<const uint8_t*>(v_cache);
-#define R4Q_ATTN(GG)                                                                        \
-  case GG:                                                                                  \
-    hipLaunchKernelGGL((attn_partial_kernel<GG>), grid, dim3(256), 0, st, qp, q_stride, kp, vp, \
-                       k_scale, v_scale, part, static_cast<uint16_t*>(out), out_stride,           \
+  // tile: the shortest that holds the longest split this launch can see
+  const int64_t lmax = seq_len_dev ? max_seq : seq_len;
+  const int64_t smax = (lmax + nsplit - 1) / nsplit;
+  const int tile = smax <= 64 ? 64 : smax <= 128 ? 128 : 256;
+#define R4Q_ATTN(GG, TT)                                                                     \
+  if (G == GG && tile == TT) {                                                               \
+    hipLaunchKernelGGL((attn_partial_kernel<GG, TT>), grid, dim3(256), 0, st, qp, q_stride, kp, \
+                       vp, k_scale, v_scale, part, static_cast<uint16_t*>(out), out_stride,      \
                        fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len, seq_len_dev, nsplit); \
-    break;
-  switch (G) {
-    R4Q_ATTN(1)
-    R4Q_ATTN(2)
-    R4Q_ATTN(4)
-    R4Q_ATTN(5)
-    R4Q_ATTN(8)
-    default:
-      return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
+    launched = true;                                                                         \
   }
+  bool launched = false;
+  R4Q_ATTN(1, 64) R4Q_ATTN(1, 128) R4Q_ATTN(1, 256)
+  R4Q_ATTN(2, 64) R4Q_ATTN(2, 128) R4Q_ATTN(2, 256)
+  R4Q_ATTN(4, 64) R4Q_ATTN(4, 128) R4Q_ATTN(4, 256)
+  R4Q_ATTN(5, 64) R4Q_ATTN(5, 128) R4Q_ATTN(5, 256)
+  R4Q_ATTN(8, 64) R4Q_ATTN(8, 128) R4Q_ATTN(8, 256)
+  if (!launched)
+    return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
 #undef R4Q_ATTN
   if (nsplit > 1)
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)H, (unsigned)B), dim3(64), 0, st, part,
