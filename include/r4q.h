@@ -28,6 +28,8 @@
  *   r4q_fp16_to_fp8      <- fp16_to_fp8             (:3611-3618)
  *   r4q_gemv             <- dbg_gemv / launch_gemv  (:3541-3550, :230-235)
  *   r4q_gemm             <- dbg_gemm / dequant_matmul_out (:3552-3561, :1973-1988)
+ *   r4q_res_rmsnorm_fwht_gemv <- fused_res_norm_fwht + launch_gemv pair
+ *                           inside the decode step
  *   r4q_rmsnorm          <- dbg_rmsnorm             (:3473-3484)
  *   r4q_res_rmsnorm      <- dbg_fused_res_norm      (:3524-3539)
  *   r4q_rmsnorm_fwht     <- fused_rmsnorm_fwht      (:1195-1237)
@@ -99,6 +101,16 @@ R4Q_API int r4q_gemv(const void* x, const void* w, const void* sz, void* y,
  * on the fly into an MFMA GEMM. */
 R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
              int64_t M, int64_t N, int64_t K, int wbits, void* stream);
+
+/* y[N] = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) (the activation
+ * of r4q_res_rmsnorm_fwht / r4q_rmsnorm_fwht, bit-identical) computed inside
+ * the GEMV; res_out = fp16(a + b) when b != NULL.  Batch 1, K <= 8192.
+ * Replaces the launch_res_norm_fwht -> launch_gemv pairs of the reference's
+ * decode step (hip:2505-2509 and the next layer's 2481 after :2518-2520;
+ * launchers :1300-1313, :230-235). */
+R4Q_API int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const void* gamma,
+                              void* res_out, float eps, const void* w, const void* sz,
+                              void* y, int64_t N, int64_t K, int wbits, void* stream);
 
 /* ------------------------------------------------------ norms / rotations */
 

@@ -39,7 +39,6 @@
 namespace r4q {
 namespace {
 
-constexpr int kMaxTile = 256;    // longest tile (positions whose scores sit in LDS)
 constexpr int kMaxSplits = 64;   // partials merged by the last workgroup
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 

@@ -139,14 +139,20 @@ int linear(const void* x, const void* w, const void* s, void* y, int64_t B, int6
 }
 
 // Optional event recorder for the per-category profile.
+// Optional per-segment timing: mark(st, cat) records an event that starts a
+// segment of category cat (kGemv, kAttn, kNorm, kRest); the segment ends at
+// the next mark.
+enum ProfCat { kGemv = 0, kAttn = 1, kNorm = 2, kRest = 3, kEnd = -1 };
 struct Prof {
   std::vector<hipEvent_t>* ev = nullptr;
-  void mark(hipStream_t st) {
+  std::vector<int>* cat = nullptr;
+  void mark(hipStream_t st, int c) {
     if (!ev) return;
     hipEvent_t e;
     (void)hipEventCreate(&e);
     (void)hipEventRecord(e, st);
     ev->push_back(e);
+    cat->push_back(c);
   }
 };
 
@@ -158,40 +164,71 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
                  hipStream_t st, Prof prof = Prof()) {
   const int64_t D = dm.D, I = dm.I;
   const float eps = dm.eps;
-  prof.mark(st);
-  R4Q_TRY(launch_rownorm(2, bf.h, nullptr, m->layers[0].in_norm, bf.rot, nullptr, B, D, eps, st));
+  // Batch 1 folds every residual + RMSNorm + FWHT into the activation
+  // staging of the GEMV that consumes it (gemv_norm_launch); batches keep
+  // the separate row-norm kernel in front of the multi-row linear.
+  const bool fused = (B == 1);
+  if (!fused) {
+    prof.mark(st, kNorm);
+    R4Q_TRY(launch_rownorm(2, bf.h, nullptr, m->layers[0].in_norm, bf.rot, nullptr, B, D, eps,
+                           st));
+  }
   for (int li = 0; li < dm.L; ++li) {
     const r4q_layer& y = m->layers[li];
-    prof.mark(st);
-    R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st));
-    prof.mark(st);
+    prof.mark(st, kGemv);
+    if (!fused) {
+      R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st));
+    } else if (li == 0) {  // input hidden state: plain RMSNorm
+      R4Q_TRY(gemv_norm_launch(bf.h, nullptr, y.in_norm, nullptr, eps, y.qkv_w, y.qkv_s, bf.qkv,
+                               dm.qkvN, D, y.qkv_bits, st));
+    } else {  // h = fp16(d + r), then RMSNorm
+      R4Q_TRY(gemv_norm_launch(bf.d, bf.r, y.in_norm, bf.h, eps, y.qkv_w, y.qkv_s, bf.qkv,
+                               dm.qkvN, D, y.qkv_bits, st));
+    }
+    prof.mark(st, kNorm);
     R4Q_TRY(launch_head_norm_rope_kv(bf.qkv, dm.qkvN, y.q_norm, y.k_norm, bf.qkv, dm.qkvN,
                                      y.k_cache, y.v_cache, y.k_scale, y.v_scale, m->rope_cos,
                                      m->rope_sin, B, dm.H, dm.Hk, eps, dm.max_seq, pos_host,
                                      pos_dev, st));
-    prof.mark(st);
+    prof.mark(st, kAttn);
     R4Q_TRY(launch_flash_decode(bf.qkv, dm.qkvN, y.k_cache, y.v_cache, y.k_scale, y.v_scale,
                                 bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
                                 nsplit, 1, bf.attn, st));
-    prof.mark(st);
+    prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
-    prof.mark(st);
-    R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
-    prof.mark(st);
-    R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
-    prof.mark(st);
+    if (fused) {  // r = fp16(o + h), then RMSNorm
+      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu, 2 * I,
+                               D, y.gu_bits, st));
+    } else {
+      prof.mark(st, kNorm);
+      R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
+      prof.mark(st, kGemv);
+      R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
+    }
+    prof.mark(st, kNorm);
     R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
+    prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
-    prof.mark(st);
-    const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm : m->layers[0].in_norm;
-    R4Q_TRY(launch_rownorm(3, bf.d, bf.r, nxt, bf.rot, bf.h, B, D, eps, st));
+    if (!fused) {
+      prof.mark(st, kNorm);
+      const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm : m->final_norm;
+      R4Q_TRY(launch_rownorm(3, bf.d, bf.r, nxt ? nxt : m->layers[0].in_norm, bf.rot, bf.h, B, D,
+                             eps, st));
+    }
   }
-  prof.mark(st);
-  if (logits) {
-    R4Q_TRY(launch_rownorm(2, bf.h, nullptr, m->final_norm, bf.rot, nullptr, B, D, eps, st));
+  // h holds the final residual stream (fp16(d + r)) once this block is done
+  if (fused && logits) {
+    prof.mark(st, kGemv);
+    R4Q_TRY(gemv_norm_launch(bf.d, bf.r, m->final_norm, bf.h, eps, m->lm_w, m->lm_s, bf.logits,
+                             m->lm_N, m->lm_K, m->lm_bits, st));
+  } else if (fused) {
+    prof.mark(st, kNorm);
+    R4Q_TRY(launch_rownorm(3, bf.d, bf.r, m->layers[0].in_norm, bf.rot, bf.h, B, D, eps, st));
+  } else if (logits) {
+    prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, m->lm_w, m->lm_s, bf.logits, B, m->lm_N, m->lm_K, m->lm_bits, st));
   }
-  prof.mark(st);
+  prof.mark(st, kEnd);
   return R4Q_OK;
 }
 
@@ -435,32 +472,25 @@ extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* 
   hipStream_t st = as_stream(stream);
   R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)dm.D * 2, hipMemcpyDeviceToDevice, st));
   std::vector<hipEvent_t> ev;
+  std::vector<int> cat;
   Prof prof;
   prof.ev = &ev;
+  prof.cat = &cat;
   int rc = enqueue_step(m, dm, 1, pos, nullptr, nullptr, nsplit, bf, m->final_norm != nullptr, st,
                         prof);
   if (rc == R4Q_OK) {
     (void)hipEventSynchronize(ev.back());
-    // events: start, then per layer 8 marks, then end-of-layers, end
-    float gemv = 0, attn = 0, norm = 0, total = 0, ms = 0;
-    for (int li = 0; li < dm.L; ++li) {
-      hipEvent_t* e = &ev[1 + 8 * li];  // e[0] = before QKV
-      (void)hipEventElapsedTime(&ms, e[0], e[1]); gemv += ms;   // QKV
-      (void)hipEventElapsedTime(&ms, e[1], e[2]); norm += ms;   // QK-norm + RoPE + KV
-      (void)hipEventElapsedTime(&ms, e[2], e[3]); attn += ms;   // flash-decode
-      (void)hipEventElapsedTime(&ms, e[3], e[4]); gemv += ms;   // O
-      (void)hipEventElapsedTime(&ms, e[4], e[5]); norm += ms;   // residual + norm
-      (void)hipEventElapsedTime(&ms, e[5], e[6]); gemv += ms;   // gate/up
-      (void)hipEventElapsedTime(&ms, e[6], e[7]); gemv += ms;   // SiLU + down
-      const hipEvent_t nxt = ev[1 + 8 * (li + 1)];
-      (void)hipEventElapsedTime(&ms, e[7], nxt); norm += ms;    // residual + norm
+    float by_cat[4] = {0.f, 0.f, 0.f, 0.f}, total = 0.f, ms = 0.f;
+    for (size_t i = 0; i + 1 < ev.size(); ++i) {
+      (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+      if (cat[i] >= 0) by_cat[cat[i]] += ms;
     }
     (void)hipEventElapsedTime(&total, ev.front(), ev.back());
     out_ms[0] = total;
-    out_ms[1] = gemv;
-    out_ms[2] = attn;
-    out_ms[3] = norm;
-    out_ms[4] = total - gemv - attn - norm;
+    out_ms[1] = by_cat[kGemv];
+    out_ms[2] = by_cat[kAttn];
+    out_ms[3] = by_cat[kNorm];
+    out_ms[4] = total - by_cat[kGemv] - by_cat[kAttn] - by_cat[kNorm];
   }
   for (hipEvent_t e : ev) (void)hipEventDestroy(e);
   return rc;

@@ -153,4 +153,44 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// 32 consecutive fp16 values <-> fp32 registers (128-bit accesses).
+__device__ __forceinline__ void load32h(const uint16_t* __restrict__ p, float* v) {
+  const u4_t* s = reinterpret_cast<const u4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u4_t d = s[i];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[8 * i + 2 * k] = h2f((uint16_t)(d[k] & 0xFFFFu));
+      v[8 * i + 2 * k + 1] = h2f((uint16_t)(d[k] >> 16));
+    }
+  }
+}
+
+__device__ __forceinline__ void store32h(uint16_t* __restrict__ p, const float* v) {
+  u4_t* d = reinterpret_cast<u4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u4_t o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = (uint32_t)f2h(v[8 * i + 2 * k]) | ((uint32_t)f2h(v[8 * i + 2 * k + 1]) << 16);
+    d[i] = o;
+  }
+}
+
+// Workgroup-wide sum in a fixed order (wave sums, then waves 0, 1, ... in
+// sequence); every thread gets the result.  `red` holds one float per wave.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  const int nw = (blockDim.x + 63) >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
 }  // namespace r4q

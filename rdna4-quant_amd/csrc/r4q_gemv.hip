@@ -61,22 +61,11 @@ __device__ __forceinline__ uint32_t pack_h(uint32_t lo16, uint32_t hi16) {
   return (lo16 & 0xFFFFu) | (hi16 << 16);
 }
 
-// Arranges chunk c of x (fp16) into the prepared layout at dst.
+// Arranges one chunk of x (E fp16 values as E/2 dwords in `raw`) into the
+// prepared layout at dst.
 template <int WBITS>
-__device__ __forceinline__ void prep_chunk(const uint16_t* __restrict__ x, int c,
-                                           uint32_t* __restrict__ dst) {
-  constexpr int E = Fmt<WBITS>::kElems;
-  const u4_t* src = reinterpret_cast<const u4_t*>(x + (int64_t)c * E);
+__device__ __forceinline__ void prep_raw(const uint32_t* raw, uint32_t* __restrict__ dst) {
   if constexpr (WBITS == 4) {
-    uint32_t raw[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u4_t v = src[i];
-      raw[4 * i + 0] = v[0];
-      raw[4 * i + 1] = v[1];
-      raw[4 * i + 2] = v[2];
-      raw[4 * i + 3] = v[3];
-    }
     float se = 0.f, so = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -99,22 +88,38 @@ __device__ __forceinline__ void prep_chunk(const uint16_t* __restrict__ x, int c
     dst[18] = 0u;
     dst[19] = 0u;
   } else if constexpr (WBITS == 8) {
-    const u4_t a = src[0], b = src[1];
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      dst[k] = a[k];
-      dst[4 + k] = b[k];
-      s += h2f((uint16_t)(a[k] & 0xFFFFu)) + h2f((uint16_t)(a[k] >> 16));
-      s += h2f((uint16_t)(b[k] & 0xFFFFu)) + h2f((uint16_t)(b[k] >> 16));
+      dst[k] = raw[k];
+      dst[4 + k] = raw[4 + k];
+      s += h2f((uint16_t)(raw[k] & 0xFFFFu)) + h2f((uint16_t)(raw[k] >> 16));
+      s += h2f((uint16_t)(raw[4 + k] & 0xFFFFu)) + h2f((uint16_t)(raw[4 + k] >> 16));
     }
     dst[8] = __float_as_uint(s);
     dst[9] = dst[10] = dst[11] = 0u;
   } else {
-    const u4_t a = src[0];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) dst[k] = a[k];
+    for (int k = 0; k < 4; ++k) dst[k] = raw[k];
   }
+}
+
+// Arranges chunk c of x (fp16 in global memory) into the prepared layout.
+template <int WBITS>
+__device__ __forceinline__ void prep_chunk(const uint16_t* __restrict__ x, int c,
+                                           uint32_t* __restrict__ dst) {
+  constexpr int E = Fmt<WBITS>::kElems;
+  const u4_t* src = reinterpret_cast<const u4_t*>(x + (int64_t)c * E);
+  uint32_t raw[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 8; ++i) {
+    const u4_t v = src[i];
+    raw[4 * i + 0] = v[0];
+    raw[4 * i + 1] = v[1];
+    raw[4 * i + 2] = v[2];
+    raw[4 * i + 3] = v[3];
+  }
+  prep_raw<WBITS>(raw, dst);
 }
 
 // acc + scale * sum over the chunk of x * (q - zp)   (FP16: acc + x . w)
@@ -204,6 +209,63 @@ __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, uint32_t
   __syncthreads();
 }
 
+// Activation of a fused-norm GEMV: x = FWHT32(fp16(a [+ b]) * rrms * gamma)
+// per 32-element chunk, rrms = 1 / sqrt(sum (a [+ b])^2 / K + eps), with
+// the arithmetic (and reduction order) of the standalone row-norm kernel, so
+// the prepared activation is bit-identical to norm-then-GEMV.  Workgroup 0
+// stores the rounded residual fp16(a + b) to res_out.  One chunk per
+// thread: K <= 32 * blockDim.x.
+struct GemvNorm {
+  const uint16_t* b;      // residual input (NULL: plain RMSNorm of x)
+  const uint16_t* gamma;  // [K] norm weight
+  uint16_t* res_out;      // [K] fp16(x + b), when b != NULL
+  float eps;
+};
+
+template <int WBITS>
+__device__ __forceinline__ void stage_x_norm(const uint16_t* __restrict__ x, const GemvNorm& nm,
+                                             uint32_t* xs, float* red, int K) {
+  constexpr int E = Fmt<WBITS>::kElems;
+  constexpr int XD = Fmt<WBITS>::kXDw;
+  const int c = threadIdx.x;
+  const bool act = c < K / 32;
+  float v[32], g[32];
+  float ss = 0.f;
+  if (act) {
+    load32h(nm.gamma + c * 32, g);  // requested with the activation
+    load32h(x + c * 32, v);
+    if (nm.b) {
+      float t[32];
+      load32h(nm.b + c * 32, t);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) v[i] += t[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
+  }
+  const float tot = block_sum(ss, red);
+  const float rrms = 1.0f / __builtin_sqrtf(tot / (float)K + nm.eps);
+  if (act) {
+    if (nm.b) {
+      // the residual is rounded to fp16 before normalisation
+      if (blockIdx.x == 0) store32h(nm.res_out + c * 32, v);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) v[i] = h2f(f2h(v[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = v[i] * rrms * g[i];
+    fwht32(v);
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      raw[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
+#pragma unroll
+    for (int sub = 0; sub < 32 / E; ++sub)
+      prep_raw<WBITS>(raw + sub * (E / 2), xs + (c * (32 / E) + sub) * XD);
+  }
+  __syncthreads();
+}
+
 template <int WBITS>
 __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, int c) {
   if constexpr (WBITS == 4) return srow[c];
@@ -280,11 +342,12 @@ __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>
   }
 }
 
-template <int WBITS, int LPR, int CPL, int UB>
+template <int WBITS, int LPR, int CPL, int UB, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x,
                                                    const uint8_t* __restrict__ w,
                                                    const uint32_t* __restrict__ sz,
-                                                   uint16_t* __restrict__ y, int N, int K) {
+                                                   uint16_t* __restrict__ y, int N, int K,
+                                                   GemvNorm nm) {
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int RPS = 256 / LPR;
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;  // waves per row
@@ -299,7 +362,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   GemvTile<WBITS, LPR, CPL, UB> ta, tb;
   gemv_load(ta, w, sz, row_bytes, nb, cpr, N, g, G, nsteps, rs, cl);
 
-  stage_x<WBITS>(x, xs, cpr);
+  if constexpr (NORM) {
+    __shared__ float nred[4];
+    stage_x_norm<WBITS>(x, nm, xs, nred, K);
+  } else {
+    stage_x<WBITS>(x, xs, cpr);
+  }
   uint32_t xr[CPL * XD];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) lds_copy<XD>(xs + min(cl + LPR * i, cpr - 1) * XD, xr + i * XD);
@@ -339,7 +407,7 @@ int env_int(const char* name, int dflt) {
 
 template <int WBITS>
 int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
-                    hipStream_t st) {
+                    const GemvNorm* norm, hipStream_t st) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int kCpl = Fmt<WBITS>::kCpl;
@@ -358,7 +426,10 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   // Workgroups: about the resident capacity (measured best: 4 per CU for
   // rows inside one wave, 2-3 per CU for rows spread over waves), with an
   // equal number of steps each.
-  const int max_wg = env_int("R4Q_GEMV_WGS", lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
+  // A fused-norm prologue is paid once per workgroup: cap at 3 per CU so it
+  // runs in a single round.
+  const int max_wg = env_int("R4Q_GEMV_WGS", norm ? (lpr == 128 ? 512 : 768)
+                                                  : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768));
   const int ub = env_int("R4Q_GEMV_UB", 1);
   const int64_t per = (nsteps + max_wg - 1) / max_wg;
   const int64_t grid = (nsteps + per - 1) / per;
@@ -370,11 +441,17 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
-#define R4Q_GEMV(L, U)                                                                     \
-  if (lpr == L && ub == U) {                                                               \
-    hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U>), gd, bd, lds_all, st, xp, wp, sp, yp, \
-                       (int)N, (int)K);                                                    \
-    return launch_status("gemv");                                                          \
+  if (norm) R4Q_REQUIRE(K <= 32 * 256, "gemv: fused norm needs K <= 8192 (K=%lld)", (long long)K);
+  const GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
+#define R4Q_GEMV(L, U)                                                                      \
+  if (lpr == L && ub == U) {                                                                \
+    if (norm)                                                                               \
+      hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, true>), gd, bd, lds_all, st, xp, wp, \
+                         sp, yp, (int)N, (int)K, nm);                                       \
+    else                                                                                    \
+      hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, false>), gd, bd, lds_all, st, xp, wp, \
+                         sp, yp, (int)N, (int)K, nm);                                       \
+    return launch_status("gemv");                                                           \
   }
   R4Q_GEMV(16, 1) R4Q_GEMV(32, 1) R4Q_GEMV(64, 1) R4Q_GEMV(128, 1) R4Q_GEMV(256, 1)
   R4Q_GEMV(16, 2) R4Q_GEMV(32, 2) R4Q_GEMV(64, 2) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
@@ -404,9 +481,22 @@ int gemv_check(const void* x, const void* w, const void* sz, const void* y, int6
 int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                 int wbits, hipStream_t st) {
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, st);
-    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, st);
-    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, st);
+    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, nullptr, st);
+    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, nullptr, st);
+    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, nullptr, st);
+  }
+}
+
+int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
+                     const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
+                     hipStream_t st) {
+  R4Q_REQUIRE(a && gamma && (!b || res_out), "gemv_norm: null pointer");
+  const GemvNorm nm{static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(gamma),
+                    static_cast<uint16_t*>(res_out), eps};
+  switch (wbits) {
+    case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, &nm, st);
+    case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, &nm, st);
+    default: return launch_gemv_fmt<16>(a, w, sz, y, N, K, &nm, st);
   }
 }
 
@@ -432,4 +522,18 @@ extern "C" int r4q_gemm(const void* x, const void* w, const void* sz, void* y, i
   R4Q_REQUIRE(M >= 1, "gemm: M must be >= 1");
   R4Q_TRY(r4q::gemv_check(x, w, sz, y, N, K, wbits));
   return r4q::gemm_launch(x, w, sz, y, M, N, K, wbits, r4q::as_stream(stream));
+}
+
+extern "C" int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const void* gamma,
+                                         void* res_out, float eps, const void* w, const void* sz,
+                                         void* y, int64_t N, int64_t K, int wbits,
+                                         void* stream) {
+  R4Q_TRY(r4q::gemv_check(a, w, sz, y, N, K, wbits));
+  R4Q_REQUIRE(gamma && (!b || res_out), "res_rmsnorm_fwht_gemv: null norm pointer");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(gamma) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(res_out) & 15) == 0,
+              "res_rmsnorm_fwht_gemv: pointers must be 16-byte aligned");
+  return r4q::gemv_norm_launch(a, b, gamma, res_out, eps, w, sz, y, N, K, wbits,
+                               r4q::as_stream(stream));
 }

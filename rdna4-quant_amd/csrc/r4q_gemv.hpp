@@ -13,6 +13,13 @@ int gemv_check(const void* x, const void* w, const void* sz, const void* y, int6
 int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                 int wbits, hipStream_t st);
 
+// y = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) computed in the
+// GEMV's activation staging (residual + RMSNorm + FWHT-32 fused); workgroup 0
+// writes res_out = fp16(a + b) when b != NULL.  K <= 8192, batch 1.
+int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
+                     const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
+                     hipStream_t st);
+
 // Row counts up to this use the weight-streaming GEMV path; above it the
 // MFMA tile GEMM with on-the-fly dequantisation.
 constexpr int64_t kSkinnyMaxRows = 16;

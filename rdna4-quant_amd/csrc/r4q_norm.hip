@@ -18,44 +18,6 @@
 namespace r4q {
 namespace {
 
-__device__ __forceinline__ void load32h(const uint16_t* __restrict__ p, float* v) {
-  const u4_t* s = reinterpret_cast<const u4_t*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u4_t d = s[i];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[8 * i + 2 * k] = h2f((uint16_t)(d[k] & 0xFFFFu));
-      v[8 * i + 2 * k + 1] = h2f((uint16_t)(d[k] >> 16));
-    }
-  }
-}
-
-__device__ __forceinline__ void store32h(uint16_t* __restrict__ p, const float* v) {
-  u4_t* d = reinterpret_cast<u4_t*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    u4_t o;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      o[k] = (uint32_t)f2h(v[8 * i + 2 * k]) | ((uint32_t)f2h(v[8 * i + 2 * k + 1]) << 16);
-    d[i] = o;
-  }
-}
-
-// Workgroup-wide sum; every thread gets the result.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int w = threadIdx.x >> 6;
-  const int nw = (blockDim.x + 63) >> 6;
-  if ((threadIdx.x & 63) == 0) red[w] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nw; ++i) t += red[i];
-  __syncthreads();
-  return t;
-}
-
 // MODE bit 0: residual input b (res_out = fp16(a + b)); bit 1: FWHT output.
 template <int MODE>
 __global__ __launch_bounds__(1024) void rownorm_kernel(const uint16_t* __restrict__ a,

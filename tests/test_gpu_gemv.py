@@ -96,3 +96,50 @@ def test_gemv_rejects_bad_k(dev):
     x = torch.zeros(48, dtype=torch.float16, device=dev)
     with pytest.raises((RuntimeError, ValueError)):
         int4_hip.dbg_gemv(x, w, s, 4, 48)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("N,K,residual", [(7168, 5120, True), (34816, 5120, False),
+                                          (257, 2048, True), (5, 96, True), (3000, 8192, False)])
+def test_fused_norm_gemv_bit_exact(dev, bits, N, K, residual):
+    """r4q_res_rmsnorm_fwht_gemv == r4q_res_rmsnorm_fwht (or r4q_rmsnorm_fwht)
+    followed by r4q_gemv, bit for bit, including the residual output."""
+    import r4q_lib as R
+    g = S.gen(3 * N + K + bits)
+    w, sz = (t if t is None else t.to(dev) for t in S.weight(N, K, bits, g))
+    a = (torch.randn(K, generator=g) * 0.7).half().to(dev)
+    b = (torch.randn(K, generator=g) * 0.7).half().to(dev) if residual else None
+    gam = S.norm_weight(K, g).to(dev)
+    eps = 1e-6
+    rot = torch.empty(K, dtype=torch.float16, device=dev)
+    res1 = torch.empty(K, dtype=torch.float16, device=dev)
+    res2 = torch.zeros(K, dtype=torch.float16, device=dev)
+    y1 = torch.empty(N, dtype=torch.float16, device=dev)
+    y2 = torch.empty(N, dtype=torch.float16, device=dev)
+    st = R.stream_handle()
+    szp = None if sz is None else sz.data_ptr()
+    if residual:
+        R.call("r4q_res_rmsnorm_fwht", a.data_ptr(), b.data_ptr(), gam.data_ptr(), rot.data_ptr(),
+               res1.data_ptr(), 1, K, eps, st)
+    else:
+        R.call("r4q_rmsnorm_fwht", a.data_ptr(), gam.data_ptr(), rot.data_ptr(), 1, K, eps, st)
+    R.call("r4q_gemv", rot.data_ptr(), w.data_ptr(), szp, y1.data_ptr(), N, K, bits, st)
+    R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), b.data_ptr() if residual else None,
+           gam.data_ptr(), res2.data_ptr() if residual else None, eps, w.data_ptr(), szp,
+           y2.data_ptr(), N, K, bits, st)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    if residual:
+        assert torch.equal(res1.view(torch.int16), res2.view(torch.int16))
+
+
+def test_fused_norm_gemv_rejects_long_rows(dev):
+    import r4q_lib as R
+    K, N = 17408, 16
+    w = torch.zeros(N, K // 2, dtype=torch.uint8, device=dev)
+    sz = torch.zeros(N, K // 16, dtype=torch.float16, device=dev)
+    a = torch.zeros(K, dtype=torch.float16, device=dev)
+    y = torch.empty(N, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError):
+        R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), None, a.data_ptr(), None, 1e-6,
+               w.data_ptr(), sz.data_ptr(), y.data_ptr(), N, K, 4, R.stream_handle())
