@@ -268,6 +268,23 @@ def main():
     tok_s = args.batch * args.steps / dt
     log(f"decode: {ms:.3f} ms/step, {tok_s:.1f} tok/s")
 
+    # prompt pass: 512 tokens through all layers + LM head for every row
+    # (config 3's GEMM shapes inside the full prefill)
+    pre_m = 512
+    ids = torch.randint(0, m["V"], (pre_m,), generator=torch.Generator().manual_seed(3)).to(dev)
+    pre_args = bench_args(m, 0)
+    lay = pre_args[:18] + pre_args[19:25]  # layer block without the position
+    had = pre_args[-1]
+    int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"], m["D"],
+                            *lay, had)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"], m["D"],
+                            *lay, had)
+    torch.cuda.synchronize()
+    pre_s = time.perf_counter() - t0
+    log(f"prefill {pre_m} tokens: {pre_s * 1e3:.1f} ms, {pre_m / pre_s:.0f} tok/s")
+
     kv_bytes = m["L"] * 2 * m["Hk"] * m["hd"] * (args.ctx + args.steps // 2) * args.batch
     step_bytes = m["wbytes"] + m["lm_bytes"] + kv_bytes
     us, alg = gemv_roofline(dev)
@@ -305,6 +322,7 @@ def main():
         "step_gbps": round(step_bytes / (ms / 1e3) / 1e9, 1),
         "step_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "int4_gemv_gbps": round(gbps, 1),
+        "prefill_512_tok_s": round(pre_m / pre_s, 1),
         "roofline": {
             "kernel": f"INT4 GEMV K=5120 -> N=17408 ({ROOFLINE_KERNEL})",
             "bound": "hbm",

@@ -48,6 +48,10 @@ PINNING = {
                     "decoded cache (int4_engine_v5.py:245); seq_len 1 closed form",
     "decode_step": "composition of the pinned functions; layer-by-layer hidden "
                    "state checks",
+    "attention_prefill": "torch F.scaled_dot_product_attention(is_causal=True, "
+                         "enable_gqa=True) (hip:2262-2264); M=1 closed form (= v)",
+    "prefill_logits": "composition of the pinned functions; row m of the prompt pass "
+                      "equals the decode step at position m on the same caches",
 }
 
 INV_SQRT32 = np.float32(0.17677669529663689)
@@ -390,6 +394,33 @@ def attention_decode(q16, k_cache, v_cache, seq_len: int, H: int, Hk: int, D: in
     return out.astype(np.float16).reshape(-1)
 
 
+def attention_prefill(q16, k16, v16, H: int, Hk: int, fwht: bool = False) -> np.ndarray:
+    """Causal GQA self-attention of M prompt rows (SDPA is_causal=True,
+    enable_gqa=True as called at hip:2262-2264 / int4_engine_v5.py:245) in
+    float64 on fp16 inputs: q16 [M, H, 128], k16/v16 [M, Hk, 128].  With
+    fwht=True the output gets the FWHT-32 rotation (hip:2269).
+    Returns fp16 [M, H*128]."""
+    q = np.asarray(q16, np.float16).astype(np.float64)
+    k = np.asarray(k16, np.float16).astype(np.float64)
+    v = np.asarray(v16, np.float16).astype(np.float64)
+    M, D = q.shape[0], q.shape[-1]
+    g = H // Hk
+    mask = np.tril(np.ones((M, M), bool))
+    out = np.empty((M, H, D), np.float64)
+    for h in range(H):
+        kh = h // g
+        sc = (q[:, h] @ k[:, kh].T) / math.sqrt(D)
+        sc = np.where(mask, sc, -np.inf)
+        sc -= sc.max(axis=1, keepdims=True)
+        p = np.exp(sc)
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, h] = p @ v[:, kh]
+    out = out.reshape(M, H * D)
+    if fwht:
+        out = fwht32_f64(out)
+    return out.astype(np.float16)
+
+
 # ------------------------------------------------------------------------ a13
 class Layer:
     """One decoder layer's tensors (numpy), mirroring int4_hip's arguments."""
@@ -443,3 +474,63 @@ def decode_step(layers, hidden16, pos: int, k_caches, v_caches, *, H, Hk, D, hid
         rot = rmsnorm_fwht(h, final_norm, eps)
         logits = gemv(rot, lm_w, lm_s, lm_bits)
     return h, logits
+
+
+# ------------------------------------------------------------------------ a15
+def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos, rope_sin,
+                   final_norm=None, lm_w=None, lm_s=None, lm_bits=4, k_caches=None,
+                   v_caches=None, k_scales=None, v_scales=None, kv_trace=None):
+    """Prompt pass over token ids [M] (int4_prefill_logits hip:2127-2320):
+    embedding, then per layer RMSNorm + FWHT, QKV, per-row head RMSNorm +
+    RoPE at position m, causal attention + FWHT, O, residual + norm + FWHT,
+    gate/up, SiLU-gate + FWHT, down, residual; final norm + FWHT and the LM
+    head for every row.  The norms apply the FWHT before the fp16 rounding
+    (the decode kernels' order).  With k_caches/v_caches ([Hk, max_seq, D]
+    uint8 per layer) the FP8 codes of positions 0..M-1 are written (K from
+    the float32 rotated values, as int4_engine_v5.py:237-242 fills the cache
+    for decode); kv_trace receives per layer (k_bytes, v_bytes, k_pre, v_pre)
+    [M, Hk, D].  Returns (hidden16 [M, hidden], logits16 [M, lm_N] or None)."""
+    ids = np.asarray(ids, np.int64).reshape(-1)
+    M = ids.size
+    x = np.asarray(embed, np.float16)[ids]
+    L = len(layers)
+    q_dim, kv_dim = H * D, Hk * D
+    rot = rmsnorm_fwht(x, layers[0].in_norm, eps)
+    for li, ly in enumerate(layers):
+        qkv = gemm(rot, ly.qkv_w, ly.qkv_s, ly.qkv_bits)
+        ks = None if k_scales is None else k_scales[li]
+        vs = None if v_scales is None else v_scales[li]
+        q = np.empty((M, H, D), np.float16)
+        k = np.empty((M, Hk, D), np.float16)
+        kb_all = np.empty((M, Hk, D), np.uint8)
+        vb_all = np.empty((M, Hk, D), np.uint8)
+        kp_all = np.empty((M, Hk, D), np.float32)
+        vp_all = np.empty((M, Hk, D), np.float32)
+        for m in range(M):
+            q_out, k_out, kb, vb, kpre, vpre = head_norm_rope_kv(
+                qkv[m], ly.q_norm, ly.k_norm, rope_cos, rope_sin, m, H, Hk, D, eps, ks, vs,
+                return_prequant=True)
+            q[m] = q_out.reshape(H, D)
+            k[m] = k_out.reshape(Hk, D)
+            kb_all[m], vb_all[m], kp_all[m], vp_all[m] = kb, vb, kpre, vpre
+        v = qkv[:, q_dim + kv_dim:].reshape(M, Hk, D)
+        if kv_trace is not None:
+            kv_trace.append((kb_all, vb_all, kp_all, vp_all))
+        if k_caches is not None:
+            k_caches[li][:, :M, :] = kb_all.transpose(1, 0, 2)
+            v_caches[li][:, :M, :] = vb_all.transpose(1, 0, 2)
+        rot = attention_prefill(q, k, v, H, Hk, fwht=True)
+        o = gemm(rot, ly.o_w, ly.o_s, ly.o_bits)
+        rot, r = res_rmsnorm_fwht(o, x, ly.post_norm, eps)
+        gu = gemm(rot, ly.gu_w, ly.gu_s, ly.gu_bits)
+        y = silu_mul_fwht(gu[:, :inter], gu[:, inter:])
+        d = gemm(y, ly.down_w, ly.down_s, ly.down_bits)
+        if li + 1 < L:
+            nxt = layers[li + 1].in_norm
+        else:
+            nxt = final_norm if final_norm is not None else layers[0].in_norm
+        rot, x = res_rmsnorm_fwht(d, r, nxt, eps)
+    logits = None
+    if final_norm is not None:
+        logits = gemm(rot, lm_w, lm_s, lm_bits)
+    return x, logits

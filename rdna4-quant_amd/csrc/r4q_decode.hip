@@ -498,6 +498,68 @@ extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* 
 
 extern "C" int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* ids, int64_t M,
                                   void* logits, int write_kv, void* stream) {
-  (void)ctx; (void)m; (void)ids; (void)M; (void)logits; (void)write_kv; (void)stream;
-  return fail(R4Q_EUNSUPPORTED, "prefill_logits: not built yet");
+  using namespace r4q;
+  R4Q_REQUIRE(ctx && ids, "prefill_logits: null argument");
+  Dims dm;
+  R4Q_TRY(validate(m, 1, dm));
+  R4Q_REQUIRE(m->embed && m->vocab >= 1, "prefill_logits: model has no embedding table");
+  R4Q_REQUIRE(M >= 1 && M <= m->rope_len, "prefill_logits: M=%lld outside [1, rope_len=%d]",
+              (long long)M, m->rope_len);
+  R4Q_REQUIRE(!write_kv || M <= m->max_seq,
+              "prefill_logits: M=%lld exceeds the KV cache capacity %d", (long long)M, m->max_seq);
+  R4Q_REQUIRE(!logits || m->final_norm, "prefill_logits: logits requested without an LM head");
+  hipStream_t st = as_stream(stream);
+  const int64_t D = dm.D, I = dm.I;
+  // token ids are checked on the host: an id outside the table would make
+  // the gather read past the embedding
+  std::vector<int64_t> hid((size_t)M);
+  R4Q_HIP_TRY(hipMemcpyAsync(hid.data(), ids, (size_t)M * 8, hipMemcpyDeviceToHost, st));
+  R4Q_HIP_TRY(hipStreamSynchronize(st));
+  for (int64_t i = 0; i < M; ++i)
+    R4Q_REQUIRE(hid[(size_t)i] >= 0 && hid[(size_t)i] < m->vocab,
+                "prefill_logits: token id %lld at row %lld outside [0, %lld)",
+                (long long)hid[(size_t)i], (long long)i, (long long)m->vocab);
+  // workspace: x, r, rot, qkv, o, gu, y, d
+  const size_t rotw = dm.qd > dm.D ? dm.qd : dm.D;
+  const size_t sizes[] = {(size_t)(M * D), (size_t)(M * D), M * rotw, (size_t)(M * dm.qkvN),
+                          (size_t)(M * D), (size_t)(M * 2 * I), (size_t)(M * I), (size_t)(M * D)};
+  size_t total = 0;
+  for (size_t sz : sizes) total += align256(sz * 2);
+  R4Q_TRY(ctx->prefill.reserve(total));
+  uint16_t* buf[8];
+  uint8_t* p = static_cast<uint8_t*>(ctx->prefill.ptr);
+  for (int i = 0; i < 8; ++i) {
+    buf[i] = reinterpret_cast<uint16_t*>(p);
+    p += align256(sizes[i] * 2);
+  }
+  uint16_t *x = buf[0], *r = buf[1], *rot = buf[2], *qkv = buf[3], *o = buf[4], *gu = buf[5],
+           *y = buf[6], *d = buf[7];
+  const float eps = dm.eps;
+  // (hip:2127-2320) embedding -> per layer: norm+FWHT, QKV, head norm +
+  // RoPE (+ FP8 KV at positions 0..M-1), causal attention + FWHT, O,
+  // residual + norm + FWHT, gate/up, SiLU-gate + FWHT, down, residual +
+  // norm + FWHT of the next layer (the last one uses the final norm); LM head
+  R4Q_TRY(launch_embed_gather(static_cast<const int64_t*>(ids), m->embed, x, M, D, st));
+  R4Q_TRY(launch_rownorm(2, x, nullptr, m->layers[0].in_norm, rot, nullptr, M, D, eps, st));
+  for (int li = 0; li < dm.L; ++li) {
+    const r4q_layer& ly = m->layers[li];
+    R4Q_TRY(gemm_launch(rot, ly.qkv_w, ly.qkv_s, qkv, M, dm.qkvN, D, ly.qkv_bits, st));
+    R4Q_TRY(launch_head_norm_rope_kv(qkv, dm.qkvN, ly.q_norm, ly.k_norm, qkv, dm.qkvN,
+                                     write_kv ? ly.k_cache : nullptr,
+                                     write_kv ? ly.v_cache : nullptr, ly.k_scale, ly.v_scale,
+                                     m->rope_cos, m->rope_sin, M, dm.H, dm.Hk, eps, dm.max_seq, 0,
+                                     nullptr, st, /*prefill_rows=*/true));
+    R4Q_TRY(launch_prefill_attention(qkv, dm.qkvN, rot, dm.qd, M, dm.H, dm.Hk, st));
+    R4Q_TRY(gemm_launch(rot, ly.o_w, ly.o_s, o, M, D, dm.qd, ly.o_bits, st));
+    R4Q_TRY(launch_rownorm(3, o, x, ly.post_norm, rot, r, M, D, eps, st));
+    R4Q_TRY(gemm_launch(rot, ly.gu_w, ly.gu_s, gu, M, 2 * I, D, ly.gu_bits, st));
+    R4Q_TRY(launch_silu(true, gu, gu + I, y, M, I, 2 * I, I, st));
+    R4Q_TRY(gemm_launch(y, ly.down_w, ly.down_s, d, M, D, I, ly.down_bits, st));
+    const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm
+                                      : (m->final_norm ? m->final_norm : m->layers[0].in_norm);
+    R4Q_TRY(launch_rownorm(3, d, r, nxt, rot, x, M, D, eps, st));
+  }
+  if (logits)
+    R4Q_TRY(gemm_launch(rot, m->lm_w, m->lm_s, logits, M, m->lm_N, m->lm_K, m->lm_bits, st));
+  return R4Q_OK;
 }

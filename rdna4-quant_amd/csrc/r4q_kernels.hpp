@@ -26,4 +26,13 @@ int launch_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw
                              int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st,
                              bool prefill_rows = false);
 
+// out[m] = table[ids[m]] for M rows of D fp16 (ids already range-checked).
+int launch_embed_gather(const int64_t* ids, const void* table, void* out, int64_t M, int64_t D,
+                        hipStream_t st);
+// Causal GQA self-attention over M prompt rows of qkv (q | k | v heads,
+// head_dim 128, row stride `stride`), FWHT-32 of each head's output,
+// out [M, out_stride] fp16.
+int launch_prefill_attention(const void* qkv, int64_t stride, void* out, int64_t out_stride,
+                             int64_t M, int64_t H, int64_t Hk, hipStream_t st);
+
 }  // namespace r4q

@@ -417,6 +417,9 @@ def decode_profile(hidden_in, embed_weight, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, 
     return [float(v) for v in out]
 
 
+_dummy_caches = {}
+
+
 def prefill_logits(input_ids, embed_weight, final_norm_w, lm_w, lm_s, lm_N, lm_K, qkv_w, qkv_s,
                    qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N, in_norm_w,
                    post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, num_heads, num_kv_heads,
@@ -430,9 +433,14 @@ def prefill_logits(input_ids, embed_weight, final_norm_w, lm_w, lm_s, lm_N, lm_K
     M = ids.numel()
     write_kv = k_caches is not None
     if not write_kv:
-        # The C ABI needs caches to describe the layers; use one-slot dummies.
-        dummy = torch.empty((1, num_kv_heads, 1, head_dim), dtype=torch.uint8,
-                            device=input_ids.device)
+        # The C ABI needs caches to describe the layers; use a one-slot dummy
+        # (kept, so repeated calls reuse one model descriptor).
+        dkey = (str(input_ids.device), num_kv_heads, head_dim)
+        dummy = _dummy_caches.get(dkey)
+        if dummy is None:
+            dummy = torch.zeros((1, num_kv_heads, 1, head_dim), dtype=torch.uint8,
+                                device=input_ids.device)
+            _dummy_caches[dkey] = dummy
         k_caches = [dummy] * len(qkv_w)
         v_caches = [dummy] * len(qkv_w)
     m = build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N,
