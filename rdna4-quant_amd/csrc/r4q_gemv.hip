@@ -503,6 +503,7 @@ int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st) {
   if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st);
+  if (gemm_skinny_ok(M, K, wbits)) return gemm_skinny_launch(x, w, sz, y, M, N, K, wbits, st);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* yp = static_cast<uint16_t*>(y);
   for (int64_t m = 0; m < M; ++m) R4Q_TRY(gemv_launch(xp + m * K, w, sz, yp + m * N, N, K, wbits, st));

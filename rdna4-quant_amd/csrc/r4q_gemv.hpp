@@ -28,6 +28,12 @@ constexpr int64_t kSkinnyMaxRows = 16;
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                      int64_t K, int wbits, hipStream_t st);
 
+// Skinny MFMA GEMM for 2 <= M <= 16 rows (weights streamed once); usable
+// when gemm_skinny_ok(M, K, wbits).
+bool gemm_skinny_ok(int64_t M, int64_t K, int wbits);
+int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                       int64_t N, int64_t K, int wbits, hipStream_t st);
+
 // y[M,N] = x[M,K] W^T; rows of x and y contiguous.
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st);

@@ -36,8 +36,41 @@ def test_prefill_gemm_ragged(dev, bits, M, N, K):
     assert rel_l2(got, want) <= TOL
 
 
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("M,N,K", [(2, 7168, 5120), (8, 17408, 5120), (8, 5120, 17408),
+                                   (16, 1000, 5120), (3, 77, 256), (5, 33, 128)])
+def test_skinny_gemm_vs_oracle(dev, bits, M, N, K):
+    """2 <= M <= 16 rows (batched decode): weights streamed once, MFMA."""
+    if K % {4: 128, 8: 64, 16: 32}[bits]:
+        pytest.skip("shape takes the per-row path")
+    got, want = _run(dev, bits, M, N, K, seed=7 * M + N + K + bits)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= TOL
+    for r in range(M):
+        assert rel_l2(got[r], want[r]) <= TOL
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_skinny_gemm_one_hot_columns_exact(dev, bits):
+    """Row r of x = e_k(r): y[r] is column k(r) of the dequantised weight,
+    bit for bit (the in-register dequantisation equals the dequant kernel)."""
+    g = S.gen(41 + bits)
+    N, K, M = 300, 1024, 8
+    w, sz = S.weight(N, K, bits, g)
+    W = O.dequant(w.numpy(), None if sz is None else sz.numpy(), bits)
+    ks = [0, 1, 4, 31, 32, 517, 1000, 1023]
+    x = torch.zeros(M, K, dtype=torch.float16)
+    for r, k in enumerate(ks):
+        x[r, k] = 1.0
+    y = int4_hip.dbg_gemm(x.to(dev), w.to(dev), None if sz is None else sz.to(dev), M, N, K)
+    y = y.cpu().numpy()
+    for r, k in enumerate(ks):
+        assert np.array_equal(y[r], W[:, k]), k
+
+
 def test_small_m_path_matches_gemv(dev):
-    """M <= 16 streams the weights per row; every row equals the GEMV."""
+    """M <= 16 rows agree with the batch-1 GEMV row by row (different
+    accumulation order: tolerance, not bits)."""
     g = S.gen(5)
     N, K = 1000, 5120
     w, sz = S.int4_weight(N, K, g)
@@ -45,4 +78,4 @@ def test_small_m_path_matches_gemv(dev):
     W, SZ, X = w.to(dev), sz.to(dev), x.to(dev)
     y = int4_hip.dbg_gemm(X, W, SZ, 8, N, K)
     for r in range(8):
-        assert torch.equal(y[r], int4_hip.dbg_gemv(X[r].contiguous(), W, SZ, N, K))
+        assert rel_l2(y[r], int4_hip.dbg_gemv(X[r].contiguous(), W, SZ, N, K)) <= 1e-3
