@@ -51,13 +51,13 @@ __device__ __forceinline__ void fp8x4_to_h2_div256(uint32_t w, uint32_t& h02, ui
   h13 = (w & m1) | ((w >> 1) & m2);
 }
 
-template <int G, int TILE>
+template <int G, int TILE, bool NORMQ>
 __global__ __launch_bounds__(256) void attn_partial_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
     float* __restrict__ part, uint16_t* __restrict__ outp,
     int64_t out_stride, int fwht, int H, int Hk, int max_seq, int L_host,
-    const int* __restrict__ L_dev, int nsplit) {
+    const int* __restrict__ L_dev, int nsplit, AttnQK qk) {
   const int sp = blockIdx.x, kh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int L = L_dev ? *L_dev : L_host;
@@ -70,6 +70,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
   __shared__ __align__(16) uint32_t pp[G][TILE / 2];
   __shared__ __align__(16) float red[8][32][G * 4];
   __shared__ float stat[G][4];  // running max, running sum, tile rescale
+  __shared__ __align__(16) uint16_t qs[NORMQ ? G : 1][128];
+  __shared__ __align__(16) uint8_t knew[128], vnew[128];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const float ks = ksc ? ksc[kh] : 1.0f;
@@ -108,25 +110,85 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     }
   };
 
-  // ---- query rows first, then the first tile: both in flight together
   uint32_t qraw[G][16];
+  if constexpr (NORMQ) {
+    // first tile in flight while the prologue normalises q (and K/V)
+    if (n > 0) {
+      load_k(0, min(TILE, n));
+      load_v(0, min(TILE, n));
+    }
+    const int pos = L - 1;
+    const bool owner = n > 0 && pos >= s0 && pos < s0 + n;  // workgroup-uniform
+    const uint16_t* row = q + b * q_stride;  // raw QKV row: q | k | v heads
+    const float c = h2f_ieee(qk.cs[(int64_t)pos * 64 + lane]);
+    const float sn = h2f_ieee(qk.sn[(int64_t)pos * 64 + lane]);
+    const int ntask = G + (owner ? 2 : 0);
+    for (int task = wave; task < ntask; task += 4) {
+      if (task < G) {
+        const uint16_t* src = row + (int64_t)(kh * G + task) * 128;
+        float lo, hi;
+        head_norm_rope_pair(h2f_ieee(src[lane]), h2f_ieee(src[lane + 64]), h2f_ieee(qk.qw[lane]),
+                            h2f_ieee(qk.qw[lane + 64]), c, sn, qk.eps, lo, hi);
+        qs[task][lane] = f2h(lo);
+        qs[task][lane + 64] = f2h(hi);
+      } else if (task == G) {
+        const uint16_t* src = row + (int64_t)(H + kh) * 128;
+        float lo, hi;
+        head_norm_rope_pair(h2f_ieee(src[lane]), h2f_ieee(src[lane + 64]), h2f_ieee(qk.kw[lane]),
+                            h2f_ieee(qk.kw[lane + 64]), c, sn, qk.eps, lo, hi);
+        const float inv = ksc ? 1.0f / ksc[kh] : 1.0f;
+        const uint8_t c0 = (uint8_t)fp8_encode(lo * inv), c1 = (uint8_t)fp8_encode(hi * inv);
+        uint8_t* kp = qk.kc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
+        kp[lane] = c0;
+        kp[lane + 64] = c1;
+        knew[lane] = c0;
+        knew[lane + 64] = c1;
+      } else {
+        const uint16_t* src = row + (int64_t)(H + Hk + kh) * 128;
+        const float inv = vsc ? 1.0f / vsc[kh] : 1.0f;
+        const uint8_t c0 = (uint8_t)fp8_encode(h2f_ieee(src[lane]) * inv);
+        const uint8_t c1 = (uint8_t)fp8_encode(h2f_ieee(src[lane + 64]) * inv);
+        uint8_t* vp = qk.vc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
+        vp[lane] = c0;
+        vp[lane + 64] = c1;
+        vnew[lane] = c0;
+        vnew[lane + 64] = c1;
+      }
+    }
+    __syncthreads();
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride + (int64_t)(kh * G + g) * 128 +
-                                                   32 * dq);
+    for (int g = 0; g < G; ++g) {
+      const u4_t* qr = reinterpret_cast<const u4_t*>(&qs[g][32 * dq]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u4_t v = qr[i];
-      qraw[g][4 * i] = v[0];
-      qraw[g][4 * i + 1] = v[1];
-      qraw[g][4 * i + 2] = v[2];
-      qraw[g][4 * i + 3] = v[3];
+      for (int i = 0; i < 4; ++i) {
+        const u4_t v = qr[i];
+        qraw[g][4 * i] = v[0];
+        qraw[g][4 * i + 1] = v[1];
+        qraw[g][4 * i + 2] = v[2];
+        qraw[g][4 * i + 3] = v[3];
+      }
+    }
+  } else {
+    // query rows first, then the first tile: both in flight together
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride +
+                                                     (int64_t)(kh * G + g) * 128 + 32 * dq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u4_t v = qr[i];
+        qraw[g][4 * i] = v[0];
+        qraw[g][4 * i + 1] = v[1];
+        qraw[g][4 * i + 2] = v[2];
+        qraw[g][4 * i + 3] = v[3];
+      }
+    }
+    if (n > 0) {
+      load_k(0, min(TILE, n));
+      load_v(0, min(TILE, n));
     }
   }
-  if (n > 0) {
-    load_k(0, min(TILE, n));
-    load_v(0, min(TILE, n));
-  }
+  const int pos_new = NORMQ ? L - 1 : -1;  // position whose K/V sit in knew/vnew
 
   // ---- query pairs matching the K decode order:
   // K dword j holds dims 4j..4j+3 -> pairs (4j, 4j+2), (4j+1, 4j+3)
@@ -163,8 +225,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
       float acc[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) acc[g] = 0.f;
-      const uint32_t k8[8] = {kw[pass][0][0], kw[pass][0][1], kw[pass][0][2], kw[pass][0][3],
-                              kw[pass][1][0], kw[pass][1][1], kw[pass][1][2], kw[pass][1][3]};
+      uint32_t k8[8] = {kw[pass][0][0], kw[pass][0][1], kw[pass][0][2], kw[pass][0][3],
+                        kw[pass][1][0], kw[pass][1][1], kw[pass][1][2], kw[pass][1][3]};
+      if constexpr (NORMQ) {  // the new position: codes from this launch
+        if (s0 + base + min(p, nt - 1) == pos_new) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) k8[j] = reinterpret_cast<const uint32_t*>(knew)[8 * dq + j];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         uint32_t h02, h13;
@@ -236,9 +304,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
 #pragma unroll
     for (int k = 0; k < kPairs; ++k) {
       const int i = 2 * wave + half + 8 * k;
+      uint32_t av = va[k], bv = vb[k];
+      if constexpr (NORMQ) {  // the new position: codes from this launch
+        const uint32_t nv = reinterpret_cast<const uint32_t*>(vnew)[d4];
+        if (s0 + base + min(2 * i, nt - 1) == pos_new) av = nv;
+        if (s0 + base + min(2 * i + 1, nt - 1) == pos_new) bv = nv;
+      }
       // (a0 a1 c0 c1) and (a2 a3 c2 c3): decode gives (a_d, c_d) pairs per dim
-      const uint32_t x0 = __builtin_amdgcn_perm(vb[k], va[k], 0x05040100u);
-      const uint32_t x1 = __builtin_amdgcn_perm(vb[k], va[k], 0x07060302u);
+      const uint32_t x0 = __builtin_amdgcn_perm(bv, av, 0x05040100u);
+      const uint32_t x1 = __builtin_amdgcn_perm(bv, av, 0x07060302u);
       uint32_t h0, h1, h2, h3;
       fp8x4_to_h2_div256(x0, h0, h1);
       fp8x4_to_h2_div256(x1, h2, h3);
@@ -370,7 +444,8 @@ size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit) {
 int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, const void* v_cache,
                         const float* k_scale, const float* v_scale, void* out, int64_t out_stride,
                         int64_t B, int64_t H, int64_t Hk, int64_t max_seq, int64_t seq_len,
-                        const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st) {
+                        const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st,
+                        const AttnQK* qk) {
   const int G = (int)(H / Hk);
   if (nsplit < 1 || nsplit > kMaxSplits)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: %d splits outside [1, %d]", nsplit, kMaxSplits);
@@ -384,12 +459,19 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   const int64_t lmax = seq_len_dev ? max_seq : seq_len;
   const int64_t smax = (lmax + nsplit - 1) / nsplit;
   const int tile = smax <= 64 ? 64 : smax <= 128 ? 128 : 256;
-#define R4Q_ATTN(GG, TT)                                                                     \
-  if (G == GG && tile == TT) {                                                               \
-    hipLaunchKernelGGL((attn_partial_kernel<GG, TT>), grid, dim3(256), 0, st, qp, q_stride, kp, \
-                       vp, k_scale, v_scale, part, static_cast<uint16_t*>(out), out_stride,      \
-                       fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len, seq_len_dev, nsplit); \
-    launched = true;                                                                         \
+#define R4Q_ATTN(GG, TT)                                                                      \
+  if (G == GG && tile == TT) {                                                                \
+    if (qk)                                                                                   \
+      hipLaunchKernelGGL((attn_partial_kernel<GG, TT, true>), grid, dim3(256), 0, st, qp,       \
+                         q_stride, kp, vp, k_scale, v_scale, part,                            \
+                         static_cast<uint16_t*>(out), out_stride, fwht, (int)H, (int)Hk,      \
+                         (int)max_seq, (int)seq_len, seq_len_dev, nsplit, *qk);               \
+    else                                                                                      \
+      hipLaunchKernelGGL((attn_partial_kernel<GG, TT, false>), grid, dim3(256), 0, st, qp,      \
+                         q_stride, kp, vp, k_scale, v_scale, part,                            \
+                         static_cast<uint16_t*>(out), out_stride, fwht, (int)H, (int)Hk,      \
+                         (int)max_seq, (int)seq_len, seq_len_dev, nsplit, AttnQK{});           \
+    launched = true;                                                                          \
   }
   bool launched = false;
   R4Q_ATTN(1, 64) R4Q_ATTN(1, 128) R4Q_ATTN(1, 256)

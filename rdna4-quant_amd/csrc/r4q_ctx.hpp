@@ -39,10 +39,28 @@ int attn_num_splits(int64_t seq_len, int64_t B, int64_t Hk);
 size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit);
 // Enqueues partial + combine; seq_len_dev != nullptr: length read on device
 // (nsplit must then cover the largest length: seq_len <= 256 * nsplit).
+// Fused decode-step prologue (NORMQ): q of the workgroup's query heads and
+// the new position's K/V come raw from the QKV projection row; the
+// workgroup applies the head RMSNorm + RoPE (head_norm_rope_pair, the
+// arithmetic of the standalone kernel) and the one holding position L-1
+// writes that position's FP8 K/V codes and uses them for its own tile.
+struct AttnQK {
+  const uint16_t* qw;  // [128] q norm weight
+  const uint16_t* kw;  // [128] k norm weight
+  const uint16_t* cs;  // RoPE tables [positions, 64]
+  const uint16_t* sn;
+  uint8_t* kc;         // caches to write at position L-1
+  uint8_t* vc;
+  float eps;
+};
+
+// qk == nullptr: q rows are final (normed, rotated) queries.  Otherwise q
+// rows are raw QKV projection rows and the fused prologue above runs.
 int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, const void* v_cache,
                         const float* k_scale, const float* v_scale, void* out, int64_t out_stride,
                         int64_t B, int64_t H, int64_t Hk, int64_t max_seq, int64_t seq_len,
-                        const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st);
+                        const int* seq_len_dev, int nsplit, int fwht, float* ws, hipStream_t st,
+                        const AttnQK* qk = nullptr);
 
 }  // namespace r4q
 

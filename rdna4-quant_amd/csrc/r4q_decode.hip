@@ -185,15 +185,16 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
       R4Q_TRY(gemv_norm_launch(bf.d, bf.r, y.in_norm, bf.h, eps, y.qkv_w, y.qkv_s, bf.qkv,
                                dm.qkvN, D, y.qkv_bits, st));
     }
-    prof.mark(st, kNorm);
-    R4Q_TRY(launch_head_norm_rope_kv(bf.qkv, dm.qkvN, y.q_norm, y.k_norm, bf.qkv, dm.qkvN,
-                                     y.k_cache, y.v_cache, y.k_scale, y.v_scale, m->rope_cos,
-                                     m->rope_sin, B, dm.H, dm.Hk, eps, dm.max_seq, pos_host,
-                                     pos_dev, st));
+    // head RMSNorm + RoPE of q/k and the FP8 K/V write at pos run in the
+    // attention kernel's prologue (raw QKV rows in)
     prof.mark(st, kAttn);
+    const AttnQK qk{static_cast<const uint16_t*>(y.q_norm), static_cast<const uint16_t*>(y.k_norm),
+                    static_cast<const uint16_t*>(m->rope_cos),
+                    static_cast<const uint16_t*>(m->rope_sin), static_cast<uint8_t*>(y.k_cache),
+                    static_cast<uint8_t*>(y.v_cache), eps};
     R4Q_TRY(launch_flash_decode(bf.qkv, dm.qkvN, y.k_cache, y.v_cache, y.k_scale, y.v_scale,
                                 bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
-                                nsplit, 1, bf.attn, st));
+                                nsplit, 1, bf.attn, st, &qk));
     prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
     if (fused) {  // r = fp16(o + h), then RMSNorm

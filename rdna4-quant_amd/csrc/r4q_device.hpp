@@ -153,6 +153,30 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Per-head RMSNorm factor, one wave per head of 128 where lane l owns
+// elements l and l + 64: 1 / sqrt(sum x^2 / 128 + eps) with the canonical
+// wave reduction.
+__device__ __forceinline__ float head_rrms(float x0, float x1, float eps) {
+#pragma clang fp contract(off)
+  const float t = x0 * x0 + x1 * x1;
+  const float ss = wave_sum(t);
+  return 1.0f / __builtin_sqrtf(ss / 128.0f + eps);
+}
+
+// Head RMSNorm + half-split RoPE of elements (l, l + 64), no fused
+// multiply-add: ne = (x0*rr)*w0, no = (x1*rr)*w1, lo = ne*c - no*s,
+// hi = no*c + ne*s.
+__device__ __forceinline__ void head_norm_rope_pair(float x0, float x1, float w0, float w1,
+                                                    float c, float s, float eps, float& lo,
+                                                    float& hi) {
+#pragma clang fp contract(off)
+  const float rr = head_rrms(x0, x1, eps);
+  const float ne = (x0 * rr) * w0;
+  const float no = (x1 * rr) * w1;
+  lo = ne * c - no * s;
+  hi = no * c + ne * s;
+}
+
 // 32 consecutive fp16 values <-> fp32 registers (128-bit accesses).
 __device__ __forceinline__ void load32h(const uint16_t* __restrict__ p, float* v) {
   const u4_t* s = reinterpret_cast<const u4_t*>(p);

@@ -101,13 +101,8 @@ __global__ __launch_bounds__(256) void silu_kernel(const uint16_t* g, const uint
 }
 
 // ------------------------------------------------------------ per-head ops
-// One wave per head of 128: lane l owns elements l and l + 64.
-__device__ __forceinline__ float head_rrms(float x0, float x1, float eps) {
-#pragma clang fp contract(off)
-  const float t = x0 * x0 + x1 * x1;
-  const float ss = wave_sum(t);
-  return 1.0f / __builtin_sqrtf(ss / 128.0f + eps);
-}
+// One wave per head of 128: lane l owns elements l and l + 64 (head_rrms in
+// r4q_device.hpp).
 
 __global__ __launch_bounds__(64) void head_rmsnorm_kernel(const uint16_t* __restrict__ q,
                                                           const uint16_t* __restrict__ k,
@@ -170,12 +165,9 @@ __global__ __launch_bounds__(64) void head_norm_rope_kv_kernel(
     const bool isq = h < H;
     const uint16_t* src = row + h * 128;  // q heads, then k heads
     const uint16_t* w = isq ? qw : kw;
-    const float x0 = h2f_ieee(src[l]), x1 = h2f_ieee(src[l + 64]);
-    const float rr = head_rrms(x0, x1, eps);
-    const float ne = (x0 * rr) * h2f_ieee(w[l]);
-    const float no = (x1 * rr) * h2f_ieee(w[l + 64]);
-    const float lo = ne * c - no * s;
-    const float hi = no * c + ne * s;
+    float lo, hi;
+    head_norm_rope_pair(h2f_ieee(src[l]), h2f_ieee(src[l + 64]), h2f_ieee(w[l]),
+                        h2f_ieee(w[l + 64]), c, s, eps, lo, hi);
     uint16_t* dst = qo + b * qo_stride + h * 128;
     dst[l] = f2h(lo);
     dst[l + 64] = f2h(hi);

@@ -76,7 +76,25 @@ def test_batch_rows_equal_single_rows(dev):
         m.k_caches = [torch.from_numpy(m.kc_np[li, b:b + 1].copy()).to(dev) for li in range(m.L)]
         m.v_caches = [torch.from_numpy(m.vc_np[li, b:b + 1].copy()).to(dev) for li in range(m.L)]
         single = step_logits(m, h[b:b + 1].to(dev), 7).cpu()
-        assert rel_l2(batched[b], single[0]) <= 1e-3
+        # batched rows take the skinny MFMA GEMM and separate norms, single
+        # rows the fused-norm GEMV: same math, different accumulation order
+        assert rel_l2(batched[b], single[0]) <= TOL
+
+
+def test_batch_rows_vs_oracle(dev):
+    m = build(dev, D=256, I=512, H=8, Hk=2, L=2, vocab=400, max_seq=48, seed=19, batch=4, fill=9,
+              bits={(1, "gu"): 8})
+    h = _hidden(m, 5, rows=4)
+    pos = 9
+    batched = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(4, -1)
+    for b in range(4):
+        kc = [m.kc_np[li, b].copy() for li in range(m.L)]
+        vc = [m.vc_np[li, b].copy() for li in range(m.L)]
+        forced, trace = gpu_kv_at(m, pos, b), []
+        _, want = oracle_step(m, h[b].numpy().reshape(-1), pos, kc, vc, b=b, forced_kv=forced,
+                              kv_trace=trace)
+        check_forced_kv(forced, trace)
+        assert rel_l2(batched[b], want) <= TOL, b
 
 
 @pytest.mark.parametrize("D,I,H,Hk,vocab", [(256, 512, 4, 2, 300), (5120, 17408, 40, 8, 2048)])
