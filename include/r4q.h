@@ -30,6 +30,7 @@
  *   r4q_gemm             <- dbg_gemm / dequant_matmul_out (:3552-3561, :1973-1988)
  *   r4q_res_rmsnorm_fwht_gemv <- fused_res_norm_fwht + launch_gemv pair
  *                           inside the decode step
+ *   r4q_gate_up_silu_fwht <- launch_gemv (gate_up) + silu_hadamard_ds pair
  *   r4q_rmsnorm          <- dbg_rmsnorm             (:3473-3484)
  *   r4q_res_rmsnorm      <- dbg_fused_res_norm      (:3524-3539)
  *   r4q_rmsnorm_fwht     <- fused_rmsnorm_fwht      (:1195-1237)
@@ -111,6 +112,18 @@ R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
 R4Q_API int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const void* gamma,
                               void* res_out, float eps, const void* w, const void* sz,
                               void* y, int64_t N, int64_t K, int wbits, void* stream);
+
+/* The gate/up projection with the SiLU-gate folded in: [g; u] = W x with
+ * W's rows [gate (I); up (I)], x = r4q_res_rmsnorm_fwht_gemv's activation
+ * (gamma != NULL) or a itself (gamma == NULL, b and res_out unused), then
+ * y[I] = fp16(FWHT32(silu(fp16(g)) * fp16(u))) -- bit-identical to the GEMV
+ * followed by r4q_silu_mul_fwht.  Batch 1; I % 32 == 0; INT4 / INT8 with
+ * K <= 5120-style rows (at most 64 lanes of 5 chunks per row).
+ * Replaces the launch_gemv (gate_up) -> silu_hadamard_ds pair of the
+ * reference's decode step (hip:2509-2513). */
+R4Q_API int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* gamma,
+                          void* res_out, float eps, const void* w, const void* sz,
+                          void* y, int64_t I, int64_t K, int wbits, void* stream);
 
 /* ------------------------------------------------------ norms / rotations */
 

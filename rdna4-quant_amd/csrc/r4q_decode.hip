@@ -197,17 +197,25 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
                                 nsplit, 1, bf.attn, st, &qk));
     prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
-    if (fused) {  // r = fp16(o + h), then RMSNorm
-      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu, 2 * I,
-                               D, y.gu_bits, st));
+    // gate/up: r = fp16(o + h), RMSNorm + FWHT in the staging and, for
+    // INT4/INT8, the SiLU-gate + FWHT in the epilogue (y written directly)
+    const bool silu_fused = fused && y.gu_bits != 16 && gemv_silu_ok(2 * I, D, y.gu_bits);
+    if (silu_fused) {
+      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.y, 2 * I,
+                               D, y.gu_bits, st, true));
     } else {
+      if (fused) {
+        R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu,
+                                 2 * I, D, y.gu_bits, st));
+      } else {
+        prof.mark(st, kNorm);
+        R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
+        prof.mark(st, kGemv);
+        R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
+      }
       prof.mark(st, kNorm);
-      R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
-      prof.mark(st, kGemv);
-      R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
+      R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
     }
-    prof.mark(st, kNorm);
-    R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
     prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
     if (!fused) {

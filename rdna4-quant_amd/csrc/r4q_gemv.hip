@@ -276,11 +276,11 @@ __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, i
 // Rows are processed in "steps" of RPS = 256/LPR rows per workgroup: LPR
 // lanes share a row (LPR <= 64: inside one wave; 128/256: 2/4 waves) and
 // lane `cl` of a row owns chunk columns cl + LPR*i, i < CPL (columns past the
-// row end are masked).  Workgroup g takes steps g, g + grid, ...; UB steps
-// form a batch and the next batch's weight loads are issued before the
-// current batch is computed (two register buffers).  The first batch is
-// requested before the activation is staged, so that staging hides behind
-// the weight stream.
+// row end are masked).  A RowMap gives the first row of the workgroup's k-th
+// step; UB consecutive steps form a batch and the next batch's weight loads
+// are issued before the current batch is computed (two register buffers).
+// The first batch is requested before the activation is staged, so that
+// staging hides behind the weight stream.
 template <int WBITS, int LPR, int CPL, int UB>
 struct GemvTile {
   static constexpr int RPS = 256 / LPR;
@@ -288,17 +288,39 @@ struct GemvTile {
   uint32_t s2[UB][CPL];
 };
 
-template <int WBITS, int LPR, int CPL, int UB>
+// Linear map: workgroup g takes global steps g, g + G, ...  SiLU map (gate /
+// up halves of a [2I] output): a unit is 32 gate rows and the 32 up rows of
+// the same indices; workgroup g takes units g, g + G, ..., each as SPU
+// consecutive steps (gate rows first).
+template <int RPS, bool SILU>
+struct RowMap {
+  int g, G, nsteps;  // linear
+  int I, nunits;     // SiLU: I = N / 2, nunits = I / 32
+  static constexpr int SPU = 64 / RPS;
+  __device__ int nlocal() const {
+    if constexpr (SILU) return g < nunits ? ((nunits - g + G - 1) / G) * SPU : 0;
+    else return g < nsteps ? (nsteps - g + G - 1) / G : 0;
+  }
+  __device__ int row0(int k) const {
+    if constexpr (SILU) {
+      const int u = g + G * (k / SPU), sub = k % SPU;
+      return sub < SPU / 2 ? 32 * u + RPS * sub : I + 32 * u + RPS * (sub - SPU / 2);
+    } else {
+      return (g + G * k) * RPS;
+    }
+  }
+};
+
+template <int WBITS, int LPR, int CPL, int UB, class Map>
 __device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
                                           const uint8_t* __restrict__ w,
                                           const uint32_t* __restrict__ sz, int64_t row_bytes,
-                                          int nb, int cpr, int N, int step0, int stride,
-                                          int nsteps, int rs, int cl) {
-  constexpr int RPS = 256 / LPR;
+                                          int nb, int cpr, int N, const Map& map, int k0,
+                                          int nloc, int rs, int cl) {
 #pragma unroll
   for (int j = 0; j < UB; ++j) {
-    const int step = min(step0 + j * stride, nsteps - 1);  // clamped: in bounds
-    const int rowc = min(step * RPS + rs, N - 1);
+    const int k = min(k0 + j, nloc - 1);  // clamped: in bounds
+    const int rowc = min(map.row0(k) + rs, N - 1);
     const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes);
     const uint32_t* srow = sz + (int64_t)rowc * nb;
 #pragma unroll
@@ -310,21 +332,41 @@ __device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
   }
 }
 
+// y[32u + i] = fp16(FWHT32(silu(g_i) * u_i)) for one SiLU unit whose
+// fp16-rounded gate/up rows sit in ut[0..31] / ut[32..63]; the arithmetic of
+// silu_kernel<true>, with the butterflies across lanes 0..31 of wave 0.
+__device__ __forceinline__ void silu_unit(const float* ut, uint16_t* __restrict__ y, int u) {
+#pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
+  if (threadIdx.x >= 64) return;
+  const int i = threadIdx.x & 31;
+  const float gv = ut[i], uv = ut[32 + i];
+  float v = gv / (1.0f + expf(-gv)) * uv;
+#pragma unroll
+  for (int bit = 1; bit <= 16; bit <<= 1) {
+    const float o = __shfl_xor(v, bit);
+    v = (i & bit) ? o - v : v + o;
+  }
+  v *= kInvSqrt32;
+  if (threadIdx.x < 32) y[32 * u + i] = f2h(v);
+}
+
 // Computes the UB steps of a batch.  Rows spread over several waves leave
 // one partial per (step, wave) in `red` (indexed by the step's ordinal k in
-// this workgroup); they are combined once, after the last batch.
-template <int WBITS, int LPR, int CPL, int UB>
+// this workgroup); they are combined once, after the last batch.  In the
+// SiLU map each row's fp16-rounded result goes to the unit buffer `ut`, and
+// the unit's last step writes its 32 outputs.
+template <int WBITS, int LPR, int CPL, int UB, class Map, bool SILU>
 __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>& t,
                                              const uint32_t* __restrict__ xr,
-                                             uint16_t* __restrict__ y, float* red, int cpr,
-                                             int N, int step0, int k0, int stride, int nsteps,
+                                             uint16_t* __restrict__ y, float* red, float* ut,
+                                             int cpr, int N, const Map& map, int k0, int nloc,
                                              int rs, int cl) {
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int RPS = 256 / LPR;
 #pragma unroll
   for (int j = 0; j < UB; ++j) {
-    const int step = step0 + j * stride;
-    if (step >= nsteps) break;  // workgroup-uniform
+    const int k = k0 + j;
+    if (k >= nloc) break;  // workgroup-uniform
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
@@ -332,35 +374,54 @@ __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>
         acc = chunk_dot<WBITS>(t.wq[j][i], t.s2[j][i], xr + i * XD, acc);
     }
     if constexpr (LPR <= 64) {
-      const int row = step * RPS + rs;
       const float total = reduce_lr(acc, LPR);
-      if (row < N && cl == 0) y[row] = f2h(total);
+      if constexpr (SILU) {
+        constexpr int SPU = Map::SPU;
+        const int sub = k % SPU;
+        const int slot = (k / SPU) & 1;
+        const int idx = sub < SPU / 2 ? RPS * sub + rs : 32 + RPS * (sub - SPU / 2) + rs;
+        if (cl == 0) ut[slot * 64 + idx] = h2f(f2h(total));
+        if (sub == SPU - 1) {  // unit complete (workgroup-uniform)
+          __syncthreads();
+          silu_unit(ut + slot * 64, y, map.g + map.G * (k / SPU));
+        }
+      } else {
+        const int row = map.row0(k) + rs;
+        if (row < N && cl == 0) y[row] = f2h(total);
+      }
     } else {
       const float total = reduce_lr(acc, 64);
-      if ((threadIdx.x & 63) == 0) red[(k0 + j) * 4 + (threadIdx.x >> 6)] = total;
+      if ((threadIdx.x & 63) == 0) red[k * 4 + (threadIdx.x >> 6)] = total;
     }
   }
 }
 
-template <int WBITS, int LPR, int CPL, int UB, bool NORM>
+template <int WBITS, int LPR, int CPL, int UB, bool NORM, bool SILU>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x,
                                                    const uint8_t* __restrict__ w,
                                                    const uint32_t* __restrict__ sz,
                                                    uint16_t* __restrict__ y, int N, int K,
                                                    GemvNorm nm) {
+  static_assert(!SILU || LPR <= 64, "the SiLU epilogue needs rows inside one wave");
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int RPS = 256 / LPR;
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;  // waves per row
   extern __shared__ __align__(16) uint32_t xs[];
+  __shared__ float ut[SILU ? 128 : 1];
   const int cpr = K / Fmt<WBITS>::kElems;
   const int nb = K / 32;
   const int64_t row_bytes = (int64_t)K * WBITS / 8;
-  const int nsteps = (N + RPS - 1) / RPS;
   const int rs = threadIdx.x / LPR, cl = threadIdx.x % LPR;
-  const int g = blockIdx.x, G = gridDim.x;
+  RowMap<RPS, SILU> map;
+  map.g = blockIdx.x;
+  map.G = gridDim.x;
+  map.nsteps = (N + RPS - 1) / RPS;
+  map.I = N / 2;
+  map.nunits = N / 64;
+  const int nloc = map.nlocal();
 
   GemvTile<WBITS, LPR, CPL, UB> ta, tb;
-  gemv_load(ta, w, sz, row_bytes, nb, cpr, N, g, G, nsteps, rs, cl);
+  if (nloc > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, 0, nloc, rs, cl);
 
   if constexpr (NORM) {
     __shared__ float nred[4];
@@ -375,23 +436,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   float* red = reinterpret_cast<float*>(xs);
   if constexpr (WPR > 1) __syncthreads();
 
-  const int batch = UB * G;
-  int k = 0;
-  for (int s0 = g; s0 < nsteps; s0 += 2 * batch, k += 2 * UB) {
-    if (s0 + batch < nsteps)
-      gemv_load(tb, w, sz, row_bytes, nb, cpr, N, s0 + batch, G, nsteps, rs, cl);
-    gemv_compute(ta, xr, y, red, cpr, N, s0, k, G, nsteps, rs, cl);
-    if (s0 + 2 * batch < nsteps)
-      gemv_load(ta, w, sz, row_bytes, nb, cpr, N, s0 + 2 * batch, G, nsteps, rs, cl);
-    if (s0 + batch < nsteps)
-      gemv_compute(tb, xr, y, red, cpr, N, s0 + batch, k + UB, G, nsteps, rs, cl);
+  for (int k = 0; k < nloc; k += 2 * UB) {
+    if (k + UB < nloc) gemv_load(tb, w, sz, row_bytes, nb, cpr, N, map, k + UB, nloc, rs, cl);
+    gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, SILU>, SILU>(ta, xr, y, red, ut, cpr, N, map,
+                                                              k, nloc, rs, cl);
+    if (k + 2 * UB < nloc)
+      gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, k + 2 * UB, nloc, rs, cl);
+    if (k + UB < nloc)
+      gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, SILU>, SILU>(tb, xr, y, red, ut, cpr, N,
+                                                                map, k + UB, nloc, rs, cl);
   }
   if constexpr (WPR > 1) {
     __syncthreads();
-    const int nlocal = (nsteps - g + G - 1) / G;
-    for (int e = threadIdx.x; e < nlocal * RPS; e += 256) {
+    for (int e = threadIdx.x; e < nloc * RPS; e += 256) {
       const int kk = e / RPS, r = e % RPS;
-      const int row = (g + kk * G) * RPS + r;
+      const int row = map.row0(kk) + r;
       const float* p = red + kk * 4 + r * WPR;
       const float total = WPR == 2 ? p[0] + p[1] : (p[0] + p[1]) + (p[2] + p[3]);
       if (row < N) y[row] = f2h(total);
@@ -407,7 +466,7 @@ int env_int(const char* name, int dflt) {
 
 template <int WBITS>
 int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
-                    const GemvNorm* norm, hipStream_t st) {
+                    const GemvNorm* norm, bool silu, hipStream_t st) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int kCpl = Fmt<WBITS>::kCpl;
@@ -422,7 +481,11 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   lpr = env_int("R4Q_GEMV_LPR", lpr);
   R4Q_REQUIRE(lpr * kCpl >= cpr, "gemv: K=%lld needs more than 256 lanes per row", (long long)K);
   const int rps = 256 / lpr;
-  const int64_t nsteps = (N + rps - 1) / rps;
+  if (silu)
+    R4Q_REQUIRE(lpr <= 64 && N % 64 == 0,
+                "gemv: SiLU epilogue needs N %% 64 == 0 and rows inside a wave");
+  // SiLU: work items are units of 64 rows (steps counted per unit)
+  const int64_t nsteps = silu ? N / 64 : (N + rps - 1) / rps;
   // Workgroups: about the resident capacity (measured best: 4 per CU for
   // rows inside one wave, 2-3 per CU for rows spread over waves), with an
   // equal number of steps each.
@@ -443,19 +506,31 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   auto* yp = static_cast<uint16_t*>(y);
   if (norm) R4Q_REQUIRE(K <= 32 * 256, "gemv: fused norm needs K <= 8192 (K=%lld)", (long long)K);
   const GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
+#define R4Q_GEMV_K(L, U, NRM, SIL)                                                         \
+  hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, NRM, SIL>), gd, bd, lds_all, st, xp, wp, sp, \
+                     yp, (int)N, (int)K, nm)
+  // rows inside one wave: plain, fused norm, SiLU epilogue, both
 #define R4Q_GEMV(L, U)                                                                      \
   if (lpr == L && ub == U) {                                                                \
-    if (norm)                                                                               \
-      hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, true>), gd, bd, lds_all, st, xp, wp, \
-                         sp, yp, (int)N, (int)K, nm);                                       \
-    else                                                                                    \
-      hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, false>), gd, bd, lds_all, st, xp, wp, \
-                         sp, yp, (int)N, (int)K, nm);                                       \
+    if (norm && silu) R4Q_GEMV_K(L, U, true, true);                                         \
+    else if (norm) R4Q_GEMV_K(L, U, true, false);                                           \
+    else if (silu) R4Q_GEMV_K(L, U, false, true);                                           \
+    else R4Q_GEMV_K(L, U, false, false);                                                    \
     return launch_status("gemv");                                                           \
   }
-  R4Q_GEMV(16, 1) R4Q_GEMV(32, 1) R4Q_GEMV(64, 1) R4Q_GEMV(128, 1) R4Q_GEMV(256, 1)
-  R4Q_GEMV(16, 2) R4Q_GEMV(32, 2) R4Q_GEMV(64, 2) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
+  R4Q_GEMV(16, 1) R4Q_GEMV(32, 1) R4Q_GEMV(64, 1)
+  R4Q_GEMV(16, 2) R4Q_GEMV(32, 2) R4Q_GEMV(64, 2)
 #undef R4Q_GEMV
+  // rows over 2 or 4 waves: plain or fused norm
+#define R4Q_GEMV(L, U)                                                                      \
+  if (lpr == L && ub == U) {                                                                \
+    if (norm) R4Q_GEMV_K(L, U, true, false);                                                \
+    else R4Q_GEMV_K(L, U, false, false);                                                    \
+    return launch_status("gemv");                                                           \
+  }
+  R4Q_GEMV(128, 1) R4Q_GEMV(256, 1) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
+#undef R4Q_GEMV
+#undef R4Q_GEMV_K
   return fail(R4Q_EUNSUPPORTED, "gemv: no kernel for %d lanes/row, %d steps/batch", lpr, ub);
 }
 
@@ -481,23 +556,29 @@ int gemv_check(const void* x, const void* w, const void* sz, const void* y, int6
 int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                 int wbits, hipStream_t st) {
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, nullptr, st);
-    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, nullptr, st);
-    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, nullptr, st);
+    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, nullptr, false, st);
+    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, nullptr, false, st);
+    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, nullptr, false, st);
   }
 }
 
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st) {
-  R4Q_REQUIRE(a && gamma && (!b || res_out), "gemv_norm: null pointer");
+                     hipStream_t st, bool silu) {
+  R4Q_REQUIRE(a && (!b || (gamma && res_out)), "gemv_norm: null pointer");
   const GemvNorm nm{static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(gamma),
                     static_cast<uint16_t*>(res_out), eps};
+  const GemvNorm* np = gamma ? &nm : nullptr;
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, &nm, st);
-    case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, &nm, st);
-    default: return launch_gemv_fmt<16>(a, w, sz, y, N, K, &nm, st);
+    case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, np, silu, st);
+    case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, np, silu, st);
+    default: return launch_gemv_fmt<16>(a, w, sz, y, N, K, np, silu, st);
   }
+}
+
+bool gemv_silu_ok(int64_t N, int64_t K, int wbits) {
+  const int64_t cpr = K / (wbits == 4 ? 32 : wbits == 8 ? 16 : 8);
+  return N % 64 == 0 && cpr <= 64 * 5;  // rows inside one wave (lanes per row <= 64)
 }
 
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
@@ -537,4 +618,20 @@ extern "C" int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const voi
               "res_rmsnorm_fwht_gemv: pointers must be 16-byte aligned");
   return r4q::gemv_norm_launch(a, b, gamma, res_out, eps, w, sz, y, N, K, wbits,
                                r4q::as_stream(stream));
+}
+
+extern "C" int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* gamma,
+                                     void* res_out, float eps, const void* w, const void* sz,
+                                     void* y, int64_t I, int64_t K, int wbits, void* stream) {
+  R4Q_REQUIRE(I > 0 && I % 32 == 0, "gate_up_silu_fwht: I must be a positive multiple of 32");
+  R4Q_TRY(r4q::gemv_check(a, w, sz, y, 2 * I, K, wbits));
+  R4Q_REQUIRE(wbits != 16 && r4q::gemv_silu_ok(2 * I, K, wbits),
+              "gate_up_silu_fwht: INT4 / INT8 rows of at most 320 chunks only");
+  R4Q_REQUIRE(!gamma || !b || res_out, "gate_up_silu_fwht: residual output required");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(gamma) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(res_out) & 15) == 0,
+              "gate_up_silu_fwht: pointers must be 16-byte aligned");
+  return r4q::gemv_norm_launch(a, gamma ? b : nullptr, gamma, gamma ? res_out : nullptr, eps, w,
+                               sz, y, 2 * I, K, wbits, r4q::as_stream(stream), true);
 }

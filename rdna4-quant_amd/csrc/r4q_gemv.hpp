@@ -15,10 +15,14 @@ int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N
 
 // y = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) computed in the
 // GEMV's activation staging (residual + RMSNorm + FWHT-32 fused); workgroup 0
-// writes res_out = fp16(a + b) when b != NULL.  K <= 8192, batch 1.
+// writes res_out = fp16(a + b) when b != NULL.  gamma == NULL: plain x = a.
+// K <= 8192 with a norm, batch 1.  silu: W's rows are [gate; up] (N = 2I)
+// and y[I] = fp16(FWHT32(silu(g) * u)) of the fp16-rounded rows (the
+// SiLU-gate kernel fused into the epilogue); needs gemv_silu_ok(N, K, wbits).
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st);
+                     hipStream_t st, bool silu = false);
+bool gemv_silu_ok(int64_t N, int64_t K, int wbits);
 
 // Row counts up to this use the weight-streaming GEMV path; above it the
 // MFMA tile GEMM with on-the-fly dequantisation.

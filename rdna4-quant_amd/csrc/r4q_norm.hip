@@ -88,6 +88,7 @@ template <bool FWHT>
 __global__ __launch_bounds__(256) void silu_kernel(const uint16_t* g, const uint16_t* u,
                                                    uint16_t* y, int I, int64_t in_stride,
                                                    int64_t out_stride) {
+#pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = blockIdx.y;
   if (c * 32 >= I) return;

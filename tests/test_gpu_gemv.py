@@ -143,3 +143,42 @@ def test_fused_norm_gemv_rejects_long_rows(dev):
     with pytest.raises(RuntimeError):
         R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), None, a.data_ptr(), None, 1e-6,
                w.data_ptr(), sz.data_ptr(), y.data_ptr(), N, K, 4, R.stream_handle())
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("I,K,norm", [(17408, 5120, True), (1024, 5120, False), (96, 256, True),
+                                      (64, 2048, False)])
+def test_gate_up_silu_fwht_bit_exact(dev, bits, I, K, norm):
+    """r4q_gate_up_silu_fwht == (fused-norm) GEMV into [g; u] followed by
+    r4q_silu_mul_fwht, bit for bit, including the residual output."""
+    import r4q_lib as R
+    g = S.gen(5 * I + K + bits)
+    w, sz = (t.to(dev) for t in S.weight(2 * I, K, bits, g))
+    a = (torch.randn(K, generator=g) * 0.7).half().to(dev)
+    b = (torch.randn(K, generator=g) * 0.7).half().to(dev)
+    gam = S.norm_weight(K, g).to(dev)
+    eps = 1e-6
+    gu = torch.empty(2 * I, dtype=torch.float16, device=dev)
+    y1 = torch.empty(I, dtype=torch.float16, device=dev)
+    y2 = torch.empty(I, dtype=torch.float16, device=dev)
+    res1 = torch.empty(K, dtype=torch.float16, device=dev)
+    res2 = torch.zeros(K, dtype=torch.float16, device=dev)
+    st = R.stream_handle()
+    if norm:
+        R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
+               res1.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K, bits, st)
+        R.call("r4q_gate_up_silu_fwht", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
+               res2.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), y2.data_ptr(), I, K, bits, st)
+    else:
+        R.call("r4q_gemv", a.data_ptr(), w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K,
+               bits, st)
+        R.call("r4q_gate_up_silu_fwht", a.data_ptr(), None, None, None, eps, w.data_ptr(),
+               sz.data_ptr(), y2.data_ptr(), I, K, bits, st)
+    R.call("r4q_silu_mul_fwht", gu.data_ptr(), gu[I:].data_ptr(), y1.data_ptr(), 1, I, 2 * I, I, st)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    if norm:
+        assert torch.equal(res1.view(torch.int16), res2.view(torch.int16))
+    # and against the oracle (its exp is numpy's: last-bit differences)
+    want = O.silu_mul_fwht(gu[:I].cpu().numpy(), gu[I:].cpu().numpy())
+    assert rel_l2(y2.cpu().numpy(), want) <= 1e-3
