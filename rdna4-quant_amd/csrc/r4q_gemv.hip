@@ -20,8 +20,8 @@
 //    v_perm to form (1024+q) pairs the same way.
 //  * The first batch of weight loads is issued before the activation is
 //    arranged (once per workgroup, in LDS, in that pair order with the
-//    per-chunk sums) and copied into registers; later batches are
-//    double-buffered in registers, one batch ahead of the arithmetic.
+//    per-chunk sums) and copied into registers; then one batch at a time is
+//    in flight per wave (3-4 workgroups per CU hide each other's waits).
 //  * Row partials are reduced across lanes with DPP row operations and
 //    v_readlane; rows spread over waves combine per-wave partials through
 //    LDS once, at the end of the workgroup.
@@ -277,10 +277,9 @@ __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, i
 // lanes share a row (LPR <= 64: inside one wave; 128/256: 2/4 waves) and
 // lane `cl` of a row owns chunk columns cl + LPR*i, i < CPL (columns past the
 // row end are masked).  A RowMap gives the first row of the workgroup's k-th
-// step; UB consecutive steps form a batch and the next batch's weight loads
-// are issued before the current batch is computed (two register buffers).
-// The first batch is requested before the activation is staged, so that
-// staging hides behind the weight stream.
+// step; UB consecutive steps form a batch.  The first batch is requested
+// before the activation is staged, so that staging hides behind the weight
+// stream.
 template <int WBITS, int LPR, int CPL, int UB>
 struct GemvTile {
   static constexpr int RPS = 256 / LPR;
@@ -420,7 +419,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   map.nunits = N / 64;
   const int nloc = map.nlocal();
 
-  GemvTile<WBITS, LPR, CPL, UB> ta, tb;
+  GemvTile<WBITS, LPR, CPL, UB> ta;
   if (nloc > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, 0, nloc, rs, cl);
 
   if constexpr (NORM) {
@@ -436,15 +435,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   float* red = reinterpret_cast<float*>(xs);
   if constexpr (WPR > 1) __syncthreads();
 
-  for (int k = 0; k < nloc; k += 2 * UB) {
-    if (k + UB < nloc) gemv_load(tb, w, sz, row_bytes, nb, cpr, N, map, k + UB, nloc, rs, cl);
+  // One batch in flight per wave: with ~3-4 workgroups per CU the other
+  // waves on a SIMD cover a wave's memory wait, and the chip-wide bytes in
+  // flight stay near the ~8-16 MB at which HBM streams best (measured: more
+  // in flight lowers the bandwidth).
+  for (int k = 0; k < nloc; k += UB) {
+    if (k > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, k, nloc, rs, cl);
     gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, SILU>, SILU>(ta, xr, y, red, ut, cpr, N, map,
                                                               k, nloc, rs, cl);
-    if (k + 2 * UB < nloc)
-      gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, k + 2 * UB, nloc, rs, cl);
-    if (k + UB < nloc)
-      gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, SILU>, SILU>(tb, xr, y, red, ut, cpr, N,
-                                                                map, k + UB, nloc, rs, cl);
   }
   if constexpr (WPR > 1) {
     __syncthreads();
