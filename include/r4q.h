@@ -168,8 +168,9 @@ R4Q_API int r4q_rope(const void* q, const void* k, const void* cos_t,
 /* Decode-step QK-norm + RoPE + FP8 KV write for B sequences at one position.
  * q/k/v: row b at qkv + b*qkv_stride (q [H,D] | k [Hk,D] | v [Hk,D]).
  * q_out/k_out (fp16, may alias q/k) get the normed+rotated vectors; the K and
- * V caches [B, Hk, max_seq, D] get FP8 codes at `pos`.  k_scale / v_scale are
- * [Hk] fp32 or NULL (scale 1).  Requires D == 128. */
+ * V caches [B, Hk, max_seq, D] get FP8 codes at `pos` (both NULL: no KV
+ * write, max_seq unused).  k_scale / v_scale are [Hk] fp32 or NULL (scale 1).
+ * Requires D == 128. */
 R4Q_API int r4q_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw,
                           const void* kw, void* q_out, int64_t q_out_stride,
                           void* k_cache, void* v_cache, const float* k_scale,

@@ -250,11 +250,12 @@ int check_head_norm_rope_kv(const void* qkv, const void* qw, const void* kw, con
                             const void* k_cache, const void* v_cache, const void* cos_t,
                             const void* sin_t, int64_t B, int64_t H, int64_t Hk, int64_t D,
                             int64_t max_seq, int64_t pos) {
-  R4Q_REQUIRE(qkv && qw && kw && q_out && k_cache && v_cache && cos_t && sin_t,
-              "head_norm_rope_kv: null pointer");
+  R4Q_REQUIRE(qkv && qw && kw && q_out && cos_t && sin_t, "head_norm_rope_kv: null pointer");
+  R4Q_REQUIRE((k_cache == nullptr) == (v_cache == nullptr),
+              "head_norm_rope_kv: pass both caches or neither");
   R4Q_REQUIRE(D == 128, "head_norm_rope_kv: head_dim must be 128 (got %lld)", (long long)D);
   R4Q_REQUIRE(B >= 1 && H >= 1 && Hk >= 1 && H % Hk == 0, "head_norm_rope_kv: bad head counts");
-  R4Q_REQUIRE(pos >= 0 && pos < max_seq,
+  R4Q_REQUIRE(pos >= 0 && (!k_cache || pos < max_seq),
               "head_norm_rope_kv: pos %lld outside the cache (max_seq %lld)", (long long)pos,
               (long long)max_seq);
   return R4Q_OK;

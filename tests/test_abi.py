@@ -85,3 +85,15 @@ def test_weight_bits_inference():
 def test_check_raises_runtime_error():
     with pytest.raises(RuntimeError):
         R.check(R.R4Q_EINVAL, "probe")
+
+
+def test_fused_ops_surface_matches_reference_signatures():
+    """fused_ops.py:28, 155, 184: names and parameter lists."""
+    import inspect
+    import fused_ops
+    sig = {n: list(inspect.signature(getattr(fused_ops, n)).parameters)
+           for n in ("fused_rmsnorm", "fused_qknorm_rope_decode", "fused_rope_decode")}
+    assert sig["fused_rmsnorm"] == ["x", "weight", "eps"]
+    assert sig["fused_qknorm_rope_decode"] == ["q", "k", "q_norm_weight", "k_norm_weight", "cos",
+                                               "sin", "position", "eps"]
+    assert sig["fused_rope_decode"] == ["q", "k", "cos", "sin", "position"]
