@@ -31,6 +31,7 @@
 // out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s, then the FWHT-32 in
 // registers (one thread per 32-dim chunk).
 #include <math.h>
+#include <stdlib.h>
 
 #include "r4q_ctx.hpp"
 #include "r4q_device.hpp"
@@ -39,7 +40,8 @@
 namespace r4q {
 namespace {
 
-constexpr int kMaxSplits = 64;   // partials merged by the last workgroup
+constexpr int kMaxSplits = 128;  // partials per (sequence, head)
+constexpr int kMergeChunk = 64;  // splits merged per round (one per lane)
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 
 // Four E4M3 bytes (b0 b1 b2 b3) -> fp16 pairs (b0, b2) and (b1, b3), each
@@ -399,26 +401,34 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x;
   const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
-  float ms = -INFINITY, ls = 0.f;
-  if (lane < nsplit) {
-    ms = pb[(int64_t)lane * kPart];
-    ls = pb[(int64_t)lane * kPart + 1];
-  }
-  float2 ov[kMaxSplits];
+  // splits in chunks of 64 (lane s holds split c0+s's m and l) with a
+  // running maximum; every load of a chunk is issued before its arithmetic
+  float M = -INFINITY, Ls = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
+    const int nc = min(kMergeChunk, nsplit - c0);
+    float ms = -INFINITY, ls = 0.f;
+    if (lane < nc) {
+      ms = pb[(int64_t)(c0 + lane) * kPart];
+      ls = pb[(int64_t)(c0 + lane) * kPart + 1];
+    }
+    float2 ov[kMergeChunk];
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s)
-    if (s < nsplit) ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)s * kPart + 4 + 2 * lane);
-  const float M = wave_max(ms);
-  const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
-  const float Ls = wave_sum(w * ls);
-  float a0 = 0.f, a1 = 0.f;
+    for (int s = 0; s < kMergeChunk; ++s)
+      ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(s, nc - 1)) * kPart + 4 +
+                                               2 * lane);
+    const float Mn = fmaxf(M, wave_max(ms));
+    const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);  // rescale of earlier chunks
+    const float w = (ms == -INFINITY) ? 0.f : __expf(ms - Mn);
+    Ls = __builtin_fmaf(Ls, r, wave_sum(w * ls));
+    a0 *= r;
+    a1 *= r;
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
-    if (s < nsplit) {
-      const float ws = readlane_f(w, s);
+    for (int s = 0; s < kMergeChunk; ++s) {
+      const float ws = readlane_f(w, s);  // 0 past the chunk end
       a0 = __builtin_fmaf(ws, ov[s].x, a0);
       a1 = __builtin_fmaf(ws, ov[s].y, a1);
     }
+    M = Mn;
   }
   const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
   *reinterpret_cast<uint32_t*>(outp + b * out_stride + (int64_t)h * 128 + 2 * lane) =
@@ -428,12 +438,19 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
 }  // namespace
 
 int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
-  // One split per 64 positions of the cache capacity, at most kMaxSplits
-  // (beyond that a workgroup walks several 256-position tiles).  Depends only
-  // on the cache capacity, so a captured graph stays valid as the sequence
-  // grows.
-  int64_t n = (cap_len + 63) / 64;
-  if (n > kMaxSplits) n = kMaxSplits;
+  // About 128 positions of the cache capacity per split, at most 64 splits
+  // (measured on MI355X at 2K-32K contexts, batch 1 and 8: more splits add
+  // merge traffic and per-workgroup fixed cost faster than they add
+  // parallelism).  Depends only on the cache capacity, so a captured graph
+  // stays valid as the sequence grows.
+  (void)B;
+  (void)Hk;
+  if (const char* e = getenv("R4Q_ATTN_SPLITS")) {  // tuning override
+    const int v = atoi(e);
+    if (v >= 1 && v <= kMaxSplits) return v;
+  }
+  int64_t n = (cap_len + 127) / 128;
+  if (n > 64) n = 64;
   return (int)(n < 1 ? 1 : n);
 }
 
