@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 2048]
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -260,10 +261,16 @@ def main():
     int4_hip.decode_bench_graph(h, m["embed"], args.warmup, *bench_args(m, wpos))
     torch.cuda.synchronize()
     log(f"warm-up {args.warmup} steps done")
+    # Python's cyclic garbage collector stays out of the timed region (a
+    # generation-2 pass over the model's objects takes ~40 ms of host time
+    # in which no step is enqueued), as in timeit
+    gc.collect()
+    gc.disable()
     t0 = time.perf_counter()
     int4_hip.decode_bench_graph(h, m["embed"], args.steps, *bench_args(m, args.ctx))
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    gc.enable()
     ms = dt * 1000.0 / args.steps
     tok_s = args.batch * args.steps / dt
     log(f"decode: {ms:.3f} ms/step, {tok_s:.1f} tok/s")
@@ -278,11 +285,14 @@ def main():
     int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"], m["D"],
                             *lay, had)
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
     t0 = time.perf_counter()
     int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"], m["D"],
                             *lay, had)
     torch.cuda.synchronize()
     pre_s = time.perf_counter() - t0
+    gc.enable()
     log(f"prefill {pre_m} tokens: {pre_s * 1e3:.1f} ms, {pre_m / pre_s:.0f} tok/s")
 
     kv_bytes = m["L"] * 2 * m["Hk"] * m["hd"] * (args.ctx + args.steps // 2) * args.batch
