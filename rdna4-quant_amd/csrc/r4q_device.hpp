@@ -96,6 +96,124 @@ __device__ __forceinline__ void fwht32(float* v) {
   for (int i = 0; i < 32; ++i) v[i] *= kInvSqrt32;
 }
 
+// ------------------------------------------ row-norm chunk arithmetic
+// One 32-element chunk of a (residual) RMSNorm [+ FWHT] row kept as 16
+// packed fp16 pairs, with the rounding sequence of
+//   v = fp32(a) + fp32(b);  ss += v * v;  r = fp16(v);
+//   y = fp16([FWHT32](fp32(r) * rrms * fp32(gamma)))
+// in fewer instructions: v_fma_mix_f32 reads fp16 halves directly (a * 1 + b
+// and r * rrms + (-0) round exactly once, like the fp32 add / multiply, and
+// the -0 addend keeps the sign of a zero product); r comes from
+// v_pk_add_f16, which equals fp16(fp32(a + b)) because rounding an fp16 sum
+// to fp32 first is innocuous (24 >= 2 * 11 + 2 bits); v_cvt_pk_f16_f32
+// rounds two values to nearest-even.  Both the row-norm kernel and the
+// fused-norm GEMV staging use these, so their activations stay bit-identical.
+template <bool HI>
+__device__ __forceinline__ float mix_add(uint32_t a, uint32_t b) {  // fp32(a.h) + fp32(b.h)
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]"
+        : "=v"(r) : "v"(a), "v"(b));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+template <bool HI>
+__device__ __forceinline__ float mix_sq_acc(uint32_t a, float acc) {  // fp32(a.h)^2 + acc
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel:[1,1,0] op_sel_hi:[1,1,0]"
+        : "=v"(r) : "v"(a), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %1, %2 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(a), "v"(acc));
+  return r;
+}
+template <bool HI>
+__device__ __forceinline__ float mix_mul_hf(uint32_t h, float s, float mz) {  // fp32(h.h) * s
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(r) : "v"(h), "v"(s), "v"(mz));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(s), "v"(mz));
+  return r;
+}
+template <bool HI>
+__device__ __forceinline__ float mix_mul_fh(float s, uint32_t h, float mz) {  // s * fp32(h.h)
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+        : "=v"(r) : "v"(s), "v"(h), "v"(mz));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(s), "v"(h), "v"(mz));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_add_h(uint32_t a, uint32_t b) {  // fp16 a + b, per half
+  uint32_t r;
+  asm("v_pk_add_f16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t cvt_pk_h(float lo, float hi) {  // (fp16(lo), fp16(hi))
+  uint32_t r;
+  asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+  return r;
+}
+
+__device__ __forceinline__ void load16w(const uint16_t* __restrict__ p, uint32_t* w) {
+  const u4_t* s = reinterpret_cast<const u4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u4_t d = s[i];
+    w[4 * i] = d[0];
+    w[4 * i + 1] = d[1];
+    w[4 * i + 2] = d[2];
+    w[4 * i + 3] = d[3];
+  }
+}
+__device__ __forceinline__ void store16w(uint16_t* __restrict__ p, const uint32_t* w) {
+  u4_t* d = reinterpret_cast<u4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = u4_t{w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+}
+
+// Phase 1: r = fp16(a + b) (RES) or a, and the sum over the chunk, in
+// element order, of squares of fp32(a + b) (or fp32(a)), added to ss.
+template <bool RES>
+__device__ __forceinline__ float norm_chunk_sumsq(const uint32_t* a, const uint32_t* b,
+                                                  uint32_t* r, float ss) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if constexpr (RES) {
+      const float lo = mix_add<false>(a[k], b[k]), hi = mix_add<true>(a[k], b[k]);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+      r[k] = pk_add_h(a[k], b[k]);
+    } else {
+      ss = mix_sq_acc<false>(a[k], ss);
+      ss = mix_sq_acc<true>(a[k], ss);
+      r[k] = a[k];
+    }
+  }
+  return ss;
+}
+
+// Phase 2: y = fp16 pairs of [FWHT32](fp32(r) * rrms * fp32(g)).
+template <bool FWHT>
+__device__ __forceinline__ void norm_chunk_scale(const uint32_t* r, const uint32_t* g, float rrms,
+                                                 uint32_t* y) {
+  float mz = -0.0f;
+  asm volatile("" : "+v"(mz));
+  float v[32];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    v[2 * k] = mix_mul_fh<false>(mix_mul_hf<false>(r[k], rrms, mz), g[k], mz);
+    v[2 * k + 1] = mix_mul_fh<true>(mix_mul_hf<true>(r[k], rrms, mz), g[k], mz);
+  }
+  if constexpr (FWHT) fwht32(v);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) y[k] = cvt_pk_h(v[2 * k], v[2 * k + 1]);
+}
+
 // ------------------------------------------------------- wave reductions
 // DPP controls (GFX9 encoding).
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]

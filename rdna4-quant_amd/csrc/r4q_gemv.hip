@@ -67,12 +67,15 @@ __device__ __forceinline__ uint32_t pack_h(uint32_t lo16, uint32_t hi16) {
 // prepared layout at dst.
 template <int WBITS>
 __device__ __forceinline__ void prep_raw(const uint32_t* raw, uint32_t* __restrict__ dst) {
+  // sums of x in element order; a v_dot2_f32_f16 with (1, 0) / (0, 1) / (1, 1)
+  // adds exact products, i.e. one rounding per step as in a scalar sum
+  const uint32_t one_lo = 0x00003C00u, one_hi = 0x3C000000u, one_both = 0x3C003C00u;
   if constexpr (WBITS == 4) {
     float se = 0.f, so = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      se += h2f((uint16_t)(raw[k] & 0xFFFFu));
-      so += h2f((uint16_t)(raw[k] >> 16));
+      se = __builtin_amdgcn_fdot2(as_h2(raw[k]), as_h2(one_lo), se, false);
+      so = __builtin_amdgcn_fdot2(as_h2(raw[k]), as_h2(one_hi), so, false);
     }
     // word j of the weight chunk holds elements 8j..8j+7; raw[4j + m] holds
     // elements (8j+2m, 8j+2m+1).
@@ -95,12 +98,16 @@ __device__ __forceinline__ void prep_raw(const uint32_t* raw, uint32_t* __restri
     for (int k = 0; k < 4; ++k) {
       dst[k] = raw[k];
       dst[4 + k] = raw[4 + k];
-      s += h2f((uint16_t)(raw[k] & 0xFFFFu)) + h2f((uint16_t)(raw[k] >> 16));
-      s += h2f((uint16_t)(raw[4 + k] & 0xFFFFu)) + h2f((uint16_t)(raw[4 + k] >> 16));
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      s = __builtin_amdgcn_fdot2(as_h2(raw[k]), as_h2(one_both), s, false);
     dst[8] = __float_as_uint(s);
     dst[9] = dst[10] = dst[11] = 0u;
   } else {
+    (void)one_lo;
+    (void)one_hi;
+    (void)one_both;
 #pragma unroll
     for (int k = 0; k < 4; ++k) dst[k] = raw[k];
   }
@@ -231,36 +238,26 @@ __device__ __forceinline__ void stage_x_norm(const uint16_t* __restrict__ x, con
   constexpr int XD = Fmt<WBITS>::kXDw;
   const int c = threadIdx.x;
   const bool act = c < K / 32;
-  float v[32], g[32];
+  uint32_t g[16], r[16];
   float ss = 0.f;
   if (act) {
-    load32h(nm.gamma + c * 32, g);  // requested with the activation
-    load32h(x + c * 32, v);
+    uint32_t av[16], bv[16];
+    load16w(nm.gamma + c * 32, g);  // requested with the activation
+    load16w(x + c * 32, av);
     if (nm.b) {
-      float t[32];
-      load32h(nm.b + c * 32, t);
-#pragma unroll
-      for (int i = 0; i < 32; ++i) v[i] += t[i];
+      load16w(nm.b + c * 32, bv);
+      ss = norm_chunk_sumsq<true>(av, bv, r, ss);
+    } else {
+      ss = norm_chunk_sumsq<false>(av, bv, r, ss);
     }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(v[i], v[i], ss);
   }
   const float tot = block_sum(ss, red);
   const float rrms = 1.0f / __builtin_sqrtf(tot / (float)K + nm.eps);
   if (act) {
-    if (nm.b) {
-      // the residual is rounded to fp16 before normalisation
-      if (blockIdx.x == 0) store32h(nm.res_out + c * 32, v);
-#pragma unroll
-      for (int i = 0; i < 32; ++i) v[i] = h2f(f2h(v[i]));
-    }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = v[i] * rrms * g[i];
-    fwht32(v);
+    // the residual is rounded to fp16 before normalisation
+    if (nm.b && blockIdx.x == 0) store16w(nm.res_out + c * 32, r);
     uint32_t raw[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      raw[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
+    norm_chunk_scale<true>(r, g, rrms, raw);
 #pragma unroll
     for (int sub = 0; sub < 32 / E; ++sub)
       prep_raw<WBITS>(raw + sub * (E / 2), xs + (c * (32 / E) + sub) * XD);

@@ -32,21 +32,16 @@ __global__ __launch_bounds__(1024) void rownorm_kernel(const uint16_t* __restric
   const int64_t row = blockIdx.x;
   const int nch = D / 32;
   constexpr int kMaxChunks = 2;  // chunks per thread (D <= 2 * 32 * 1024)
-  float v[kMaxChunks][32];
+  uint32_t r[kMaxChunks][16];  // fp16 pairs: a, or the rounded residual fp16(a + b)
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kMaxChunks; ++j) {
     const int c = threadIdx.x + j * blockDim.x;
     if (c < nch) {
-      load32h(a + row * D + c * 32, v[j]);
-      if constexpr (RES) {
-        float t[32];
-        load32h(b + row * D + c * 32, t);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) v[j][i] += t[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 32; ++i) ss = __builtin_fmaf(v[j][i], v[j][i], ss);
+      uint32_t av[16], bv[16];
+      load16w(a + row * D + c * 32, av);
+      if constexpr (RES) load16w(b + row * D + c * 32, bv);
+      ss = norm_chunk_sumsq<RES>(av, bv, r[j], ss);
     }
   }
   const float tot = block_sum(ss, red);
@@ -55,19 +50,13 @@ __global__ __launch_bounds__(1024) void rownorm_kernel(const uint16_t* __restric
   for (int j = 0; j < kMaxChunks; ++j) {
     const int c = threadIdx.x + j * blockDim.x;
     if (c < nch) {
-      float g[32];
-      load32h(w + c * 32, g);
-      if constexpr (RES) {
-        // residual is rounded to fp16 before normalisation (hip:1151-1153,
-        // 1178): store it and continue from the rounded value
-        store32h(res_out + row * D + c * 32, v[j]);
-#pragma unroll
-        for (int i = 0; i < 32; ++i) v[j][i] = h2f(f2h(v[j][i]));
-      }
-#pragma unroll
-      for (int i = 0; i < 32; ++i) v[j][i] = v[j][i] * rrms * g[i];
-      if constexpr (FWHT) fwht32(v[j]);
-      store32h(y + row * D + c * 32, v[j]);
+      uint32_t g[16], o[16];
+      load16w(w + c * 32, g);
+      // the residual is rounded to fp16 before normalisation (hip:1151-1153,
+      // 1178): stored, and normalised from the rounded value
+      if constexpr (RES) store16w(res_out + row * D + c * 32, r[j]);
+      norm_chunk_scale<FWHT>(r[j], g, rrms, o);
+      store16w(y + row * D + c * 32, o);
     }
   }
 }
