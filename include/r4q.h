@@ -246,6 +246,14 @@ R4Q_API int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidde
 R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                        int64_t pos, float* out_ms, void* stream);
 
+/* Measurement aid with no counterpart in the reference: reads `bytes` bytes
+ * at src (16-byte aligned) once, with the fastest plain-read layout measured
+ * on MI355X, so that a kernel's duration can be set against the HBM read
+ * floor for the same byte count.  sink: device scratch of >= 8192 bytes,
+ * normally left untouched. */
+R4Q_API int r4q_hbm_read(const void* src, int64_t bytes, void* sink, int64_t sink_bytes,
+                         void* stream);
+
 /* Prefill M tokens from position 0: embedding of ids (int64 [M]) through all
  * layers; writes logits [M, lm_N] fp16 (NULL: skip the LM head) and, when
  * write_kv != 0, the FP8 KV caches at positions 0..M-1. */

@@ -71,6 +71,7 @@ SIGNATURES = {
     "r4q_rmsnorm_fwht": [_p, _p, _p, _i64, _i64, _f32, _p],
     "r4q_res_rmsnorm_fwht": [_p, _p, _p, _p, _p, _i64, _i64, _f32, _p],
     "r4q_fwht32": [_p, _p, _i64, _p],
+    "r4q_hbm_read": [_p, _i64, _p, _i64, _p],
     "r4q_silu_mul_fwht": [_p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_silu_mul": [_p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_head_rmsnorm": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
