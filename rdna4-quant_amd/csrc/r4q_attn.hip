@@ -1,5 +1,5 @@
 // Split-K flash-decode over the FP8 E4M3 KV cache (GQA), with the log-sum-exp
-// merge and the optional FWHT-32 output rotation fused into the same launch.
+// merge and the optional FWHT-32 output rotation.
 //
 // Replaces the reference's launch_flash_decode (hip:1547-1593) with its
 // flash_decode_partial (hip:1326-1412), flash_decode_reduce (hip:1416-1463)
@@ -9,27 +9,11 @@
 // dot4_f32_fp8_fp8 instruction does not exist on gfx950), and K/V carry an
 // optional per-head fp32 scale.
 //
-// One workgroup (4 waves) per (split, kv head, sequence) walks its split in
-// 256-position tiles:
-//  * every K and V load of a tile is issued before any arithmetic (one
-//    memory latency per tile);
-//  * QK: 4 lanes per position, each owning 32 head dims; the position's 32 K
-//    bytes arrive in two 128-bit loads and are widened to fp16 by placing the
-//    E4M3 fields into fp16 fields (exact, value / 256); the GQA group's query
-//    heads live in registers as fp16 pairs so every K byte feeds all of them
-//    through v_dot2_f32_f16; the 4 partial dots are combined with DPP.
-//  * scores -> LDS; online softmax per head: tile max, running max/sum and
-//    the rescale factor of earlier tiles, fp16-rounded probabilities of
-//    position pairs -> LDS.
-//  * PV: each lane owns 4 head dims; two positions' V bytes are interleaved
-//    with v_perm so v_dot2 contracts over the position pair; the running
-//    accumulators are rescaled per tile and reduced across half-waves and
-//    waves through LDS at the end.
-// Merge: the last workgroup to finish for a (sequence, kv head) -- found with
-// a self-resetting arrival counter, no waiting -- combines the (at most 64)
-// splits while they are in cache with 128-bit loads: m* = max_s m_s,
-// out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s, then the FWHT-32 in
-// registers (one thread per 32-dim chunk).
+// attn_mfma_kernel computes one (split, KV head, sequence) per workgroup on
+// the matrix cores; attn_merge_kernel combines the splits per query head:
+// m* = max_s m_s, out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s, with the
+// FWHT-32 already applied to each o_s (it is linear).  A single split writes
+// the fp16 output directly.
 #include <math.h>
 #include <stdlib.h>
 
@@ -44,83 +28,131 @@ constexpr int kMaxSplits = 128;  // partials per (sequence, head)
 constexpr int kMergeChunk = 64;  // splits merged per round (one per lane)
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 
-// Four E4M3 bytes (b0 b1 b2 b3) -> fp16 pairs (b0, b2) and (b1, b3), each
-// value divided by 256 (exact).
-__device__ __forceinline__ void fp8x4_to_h2_div256(uint32_t w, uint32_t& h02, uint32_t& h13) {
-  uint32_t m1 = 0x80008000u, m2 = 0x3F803F80u;
-  asm volatile("" : "+v"(m1), "+v"(m2));
-  h02 = ((w << 8) & m1) | ((w << 7) & m2);
-  h13 = (w & m1) | ((w >> 1) & m2);
+// ------------------------------------------------ MFMA flash-decode partials
+// E4M3 bytes 0-1 (HI: 2-3) of w -> fp16 pair, v_cvt_scalef32_pk_f16_fp8 with
+// scale 1: exact and equal to the reference decoder (hip:71-81) for every
+// code the reference encoder emits (it flushes E <= 0 to +-0 and saturates
+// at 0x7E, so the E4M3 subnormal and 0x7F codes, which decode differently,
+// never occur in a cache).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_h2(uint32_t w) {
+  return as_u32(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
 }
 
-template <int G, int TILE, bool NORMQ>
-__global__ __launch_bounds__(256) void attn_partial_kernel(
+// 4x4 byte transpose: out[d] = byte d of in[0], in[1], in[2], in[3].
+__device__ __forceinline__ void transpose4x4(const uint32_t* in, uint32_t* out) {
+  const uint32_t a0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // in0.b0 in1.b0 in0.b1 in1.b1
+  const uint32_t a1 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // in0.b2 in1.b2 in0.b3 in1.b3
+  const uint32_t b0 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);
+  const uint32_t b1 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(b0, a0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(b0, a0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(b1, a1, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(b1, a1, 0x07060302u);
+}
+
+__device__ __forceinline__ f4_t mfma16(u4_t a, u4_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+// Flash-decode partials on the matrix cores (v_mfma_f32_16x16x32_f16), one
+// workgroup per (split, KV head, sequence).  The sequence is cut into
+// 32-position chunks dealt round-robin to the splits; each of the 4 waves
+// walks its split's chunks wave, wave + 4, ... with its own online-softmax
+// state, and the waves merge once at the end through LDS.
+// Lane l has column n = l % 16 and group g = l / 16.  Per chunk:
+//  * S^T = K Q^T for two 16-position blocks: A = K (lane: position n of the
+//    block, dims 32g .. 32g+31 over the 4 k-steps), B = Q^T (lane: head n,
+//    the same dims; heads >= G are zero).  C: lane holds head n at positions
+//    4g .. 4g+3 of the block;
+//  * online softmax per head across the 4 lanes holding it (the running
+//    output is rescaled only when a head's maximum rises), probabilities
+//    rounded to fp16 as in the reference kernel;
+//  * O += P V: A = P (lane: head n; k-slots = its 8 positions 4g+r and
+//    16+4g+r), B = V (lane: dim 8n + j for N-block j, the same positions):
+//    each lane loads 8 bytes (dims 8n .. 8n+7) of its 8 position rows and
+//    transposes them to per-dim bytes with v_perm.  C: lane holds dim 8n + j
+//    for heads 4g .. 4g+3.
+// K rows load as 32 contiguous bytes per lane and V rows as 8 (16 lanes
+// cover a 128-byte row); the next chunk's K (V) loads are issued as soon as
+// this chunk's K (V) registers are converted.
+// Prologue (NORMQ): per-head RMSNorm + RoPE of q and k, FP8 write of the new
+// K/V at position L-1 by the workgroup holding that position, which patches
+// the codes into its own (earlier issued) loads.  Epilogue: FWHT-32 per
+// 32-dim chunk, then the fp32 partial (m, l, o) or, with one split, the
+// normalised fp16 output.
+template <int G, bool NORMQ>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
-    float* __restrict__ part, uint16_t* __restrict__ outp,
-    int64_t out_stride, int fwht, int H, int Hk, int max_seq, int L_host,
-    const int* __restrict__ L_dev, int nsplit, AttnQK qk) {
+    float* __restrict__ part, uint16_t* __restrict__ outp, int64_t out_stride, int fwht, int H,
+    int Hk, int max_seq, int L_host, const int* __restrict__ L_dev, int nsplit, AttnQK qk) {
+  static_assert(G >= 1 && G <= 16, "query heads per KV head must fit 16 MFMA columns");
   const int sp = blockIdx.x, kh = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int L = L_dev ? *L_dev : L_host;
-  const int S = (L + nsplit - 1) / nsplit;
-  const int s0 = sp * S;
-  const int n = max(0, min(L, s0 + S) - s0);
+  // 32-position chunks are dealt to the splits round-robin (split sp takes
+  // chunks sp, sp + nsplit, ...), so that at any moment the workgroups of a
+  // head read one contiguous window of the cache (a plain stream for HBM)
+  // instead of nsplit separate ranges; the softmax merge does not depend on
+  // which positions a split holds.
+  const int nct = (L + 31) / 32;
+  const int nchunk = sp < nct ? (nct - 1 - sp) / nsplit + 1 : 0;  // this split's chunks
+  auto cpos = [&](int c) { return 32 * (sp + nsplit * c); };  // first position of local chunk c
 
-  // 128-bit LDS accesses below need 16-byte aligned rows
-  __shared__ __align__(16) float sc[G][TILE < 128 ? 128 : TILE];  // also the output stage
-  __shared__ __align__(16) uint32_t pp[G][TILE / 2];
-  __shared__ __align__(16) float red[8][32][G * 4];
-  __shared__ float stat[G][4];  // running max, running sum, tile rescale
   __shared__ __align__(16) uint16_t qs[NORMQ ? G : 1][128];
   __shared__ __align__(16) uint8_t knew[128], vnew[128];
+  __shared__ float wst[4][G][2];                  // per wave: max, sum
+  __shared__ __align__(16) float wo[4][G][128];  // per wave: unnormalised O
+  __shared__ __align__(16) float ostage[G][128];
+  __shared__ float fin[G][2];  // merged max, sum
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int col = lane & 15, g = lane >> 4;
   const float ks = ksc ? ksc[kh] : 1.0f;
   const float vs = vsc ? vsc[kh] : 1.0f;
-  const int64_t head_off = ((b * Hk + kh) * (int64_t)max_seq + s0) * 128;
+  const int64_t head_off = (b * Hk + kh) * (int64_t)max_seq * 128;
   const uint8_t* kbase = kc + head_off;
   const uint8_t* vbase = vc + head_off;
 
-  const int dq = t & 3;
-  const int d4 = lane & 31, half = lane >> 5;
-
-  // ---- K and V loads of a tile.  Rows past the tile end are clamped to its
-  // last row; their scores become -inf and their probabilities 0.
-  constexpr int kPass = TILE / 64;   // 64 positions per QK pass
-  constexpr int kPairs = TILE / 16;  // position pairs per (wave, half) slot
-  u4_t kw[kPass][2];
-  uint32_t va[kPairs], vb[kPairs];
-  auto load_k = [&](int base, int nt) {
+  // local chunk c: K rows cpos(c) + 16bb + col (32 bytes from dim 32g), V
+  // rows cpos(c) + vpos(s) (8 bytes from dim 8col); rows past the sequence
+  // end are clamped to its last row and masked.  Only called for c < nchunk.
+  auto vpos = [&](int s) { return s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4); };
+  // One register set per wave: the next chunk's K (V) loads are issued as
+  // soon as this chunk's K (V) registers are converted (a second set in
+  // flight measured no faster and raised register pressure).  Byte offsets
+  // are 32-bit from the workgroup's uniform row base.
+  u4_t kr0[2][2];
+  u2_t vr0[8];
+  auto load_k = [&](u4_t (&kr)[2][2], int c) {
 #pragma unroll
-    for (int pass = 0; pass < kPass; ++pass) {
-      const int p = min(pass * 64 + (t >> 2), nt - 1);
-      const u4_t* kr = reinterpret_cast<const u4_t*>(kbase + (int64_t)(base + p) * 128 + 32 * dq);
-      kw[pass][0] = __builtin_nontemporal_load(kr);
-      kw[pass][1] = __builtin_nontemporal_load(kr + 1);
+    for (int bb = 0; bb < 2; ++bb) {
+      const uint32_t p = (uint32_t)min(cpos(c) + 16 * bb + col, L - 1);
+      const u4_t* src = reinterpret_cast<const u4_t*>(kbase + (p * 128u + 32u * g));
+      kr[bb][0] = __builtin_nontemporal_load(src);
+      kr[bb][1] = __builtin_nontemporal_load(src + 1);
     }
   };
-  auto load_v = [&](int base, int nt) {
+  auto load_v = [&](u2_t (&vr)[8], int c) {
 #pragma unroll
-    for (int k = 0; k < kPairs; ++k) {
-      const int i = 2 * wave + half + 8 * k;
-      const int r0 = min(2 * i, nt - 1), r1 = min(2 * i + 1, nt - 1);
-      va[k] = __builtin_nontemporal_load(
-          reinterpret_cast<const uint32_t*>(vbase + (int64_t)(base + r0) * 128 + 4 * d4));
-      vb[k] = __builtin_nontemporal_load(
-          reinterpret_cast<const uint32_t*>(vbase + (int64_t)(base + r1) * 128 + 4 * d4));
+    for (int s = 0; s < 8; ++s) {
+      const uint32_t p = (uint32_t)min(cpos(c) + vpos(s), L - 1);
+      vr[s] = __builtin_nontemporal_load(
+          reinterpret_cast<const u2_t*>(vbase + (p * 128u + 8u * col)));
     }
   };
+  if (wave < nchunk) {  // first chunk in flight during the query prologue
+    load_k(kr0, wave);
+    load_v(vr0, wave);
+  }
 
-  uint32_t qraw[G][16];
+  // ---- query: B operands qb[j] = Q[head col][32g + 8j .. +7] (0 for col >= G)
+  u4_t qb[4];
   if constexpr (NORMQ) {
-    // first tile in flight while the prologue normalises q (and K/V)
-    if (n > 0) {
-      load_k(0, min(TILE, n));
-      load_v(0, min(TILE, n));
-    }
     const int pos = L - 1;
-    const bool owner = n > 0 && pos >= s0 && pos < s0 + n;  // workgroup-uniform
+    const bool owner = (pos >> 5) % nsplit == sp;  // holds the new position's chunk
     const uint16_t* row = q + b * q_stride;  // raw QKV row: q | k | v heads
     const float c = h2f_ieee(qk.cs[(int64_t)pos * 64 + lane]);
     const float sn = h2f_ieee(qk.sn[(int64_t)pos * 64 + lane]);
@@ -159,205 +191,179 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const u4_t* qr = reinterpret_cast<const u4_t*>(&qs[g][32 * dq]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u4_t v = qr[i];
-        qraw[g][4 * i] = v[0];
-        qraw[g][4 * i + 1] = v[1];
-        qraw[g][4 * i + 2] = v[2];
-        qraw[g][4 * i + 3] = v[3];
-      }
-    }
+    for (int j = 0; j < 4; ++j)
+      qb[j] = col < G ? *reinterpret_cast<const u4_t*>(&qs[col][32 * g + 8 * j]) : u4_t{0, 0, 0, 0};
   } else {
-    // query rows first, then the first tile: both in flight together
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const u4_t* qr = reinterpret_cast<const u4_t*>(q + b * q_stride +
-                                                     (int64_t)(kh * G + g) * 128 + 32 * dq);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u4_t v = qr[i];
-        qraw[g][4 * i] = v[0];
-        qraw[g][4 * i + 1] = v[1];
-        qraw[g][4 * i + 2] = v[2];
-        qraw[g][4 * i + 3] = v[3];
-      }
-    }
-    if (n > 0) {
-      load_k(0, min(TILE, n));
-      load_v(0, min(TILE, n));
-    }
+    for (int j = 0; j < 4; ++j)
+      qb[j] = col < G ? *reinterpret_cast<const u4_t*>(q + b * q_stride +
+                                                       (int64_t)(kh * G + col) * 128 + 32 * g +
+                                                       8 * j)
+                      : u4_t{0, 0, 0, 0};
   }
   const int pos_new = NORMQ ? L - 1 : -1;  // position whose K/V sit in knew/vnew
 
-  // ---- query pairs matching the K decode order:
-  // K dword j holds dims 4j..4j+3 -> pairs (4j, 4j+2), (4j+1, 4j+3)
-  uint32_t qp[G][16];
+  const float sscale = ks * 0.08838834764831845f;  // k_scale / sqrt(128)
+  const uint32_t ones = 0x3C003C00u;               // fp16 (1, 1)
+  float m_run = -INFINITY, l_run = 0.f;            // head col; l over this lane's positions
+  f4_t o[8];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t a = qraw[g][2 * j], c = qraw[g][2 * j + 1];
-      qp[g][2 * j] = (a & 0xFFFFu) | (c << 16);
-      qp[g][2 * j + 1] = (a >> 16) | (c & 0xFFFF0000u);
-    }
-  }
-  if (t < G) {
-    stat[t][0] = -INFINITY;
-    stat[t][1] = 0.f;
-  }
+  for (int j = 0; j < 8; ++j) o[j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  float o[G][4];
+  // one chunk from the register set (kr, vr), which then receives this
+  // wave's next chunk (c + 4)
+  auto step = [&](u4_t (&kr)[2][2], u2_t (&vr)[8], int c) {
+    const bool more = c + 4 < nchunk;  // wave-uniform
+    // ---- K -> fp16 A operands, next chunk's K in flight, S^T = K Q^T
+    u4_t ka[2][4];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[g][j] = 0.f;
-
-  const float sscale = ks * 22.627416997969522f;  // 256 / sqrt(128)
-  for (int base = 0; base < n; base += TILE) {
-    const int nt = min(TILE, n - base);
-    // (this tile's K and V were requested before the previous tile's
-    // arithmetic, or before the query prep for the first tile)
-    // ---- Q K^T, 4 lanes per position, 64 positions per pass
-#pragma unroll
-    for (int pass = 0; pass < kPass; ++pass) {
-      const int p = pass * 64 + (t >> 2);
-      float acc[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[g] = 0.f;
-      uint32_t k8[8] = {kw[pass][0][0], kw[pass][0][1], kw[pass][0][2], kw[pass][0][3],
-                        kw[pass][1][0], kw[pass][1][1], kw[pass][1][2], kw[pass][1][3]};
-      if constexpr (NORMQ) {  // the new position: codes from this launch
-        if (s0 + base + min(p, nt - 1) == pos_new) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) k8[j] = reinterpret_cast<const uint32_t*>(knew)[8 * dq + j];
+    for (int bb = 0; bb < 2; ++bb) {
+      u4_t r0 = kr[bb][0], r1 = kr[bb][1];
+      if constexpr (NORMQ) {
+        if (min(cpos(c) + 16 * bb + col, L - 1) == pos_new) {
+          r0 = *reinterpret_cast<const u4_t*>(&knew[32 * g]);
+          r1 = *reinterpret_cast<const u4_t*>(&knew[32 * g + 16]);
         }
       }
+      const uint32_t w[8] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        uint32_t h02, h13;
-        fp8x4_to_h2_div256(k8[j], h02, h13);
+      for (int j = 0; j < 4; ++j)
+        ka[bb][j] = u4_t{fp8x2_h2<false>(w[2 * j]), fp8x2_h2<true>(w[2 * j]),
+                         fp8x2_h2<false>(w[2 * j + 1]), fp8x2_h2<true>(w[2 * j + 1])};
+    }
+    if (more) load_k(kr, c + 4);
+    f4_t sacc[2];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          acc[g] = __builtin_amdgcn_fdot2(as_h2(h02), as_h2(qp[g][2 * j]), acc[g], false);
-          acc[g] = __builtin_amdgcn_fdot2(as_h2(h13), as_h2(qp[g][2 * j + 1]), acc[g], false);
+    for (int bb = 0; bb < 2; ++bb) {
+      sacc[bb] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sacc[bb] = mfma16(ka[bb][j], qb[j], sacc[bb]);
+    }
+
+    // ---- online softmax for head col over positions 32c + vpos(s)
+    float sv[8];
+    if (cpos(c) + 32 <= L) {  // wave-uniform: a full chunk
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sv[s] = sacc[s >> 2][s & 3] * sscale;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        sv[s] = (cpos(c) + vpos(s) < L) ? sacc[s >> 2][s & 3] * sscale : -INFINITY;
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int s = 1; s < 8; ++s) mx = fmaxf(mx, sv[s]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m_run, mx);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __expf(m_run - mn);
+    // O needs rescaling only where a head's running max rose (O is zero
+    // before the first finite max); exp(0) == 1 exactly elsewhere
+    const bool rescale =
+        __builtin_amdgcn_ballot_w64(m_run != -INFINITY && mn != m_run) != 0;  // wave-uniform
+    u4_t pa;  // fp16 probabilities, k-slot s = position vpos(s)
+    float lp = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p0 = (mn == -INFINITY) ? 0.f : __expf(sv[2 * i] - mn);
+      const float p1 = (mn == -INFINITY) ? 0.f : __expf(sv[2 * i + 1] - mn);
+      pa[i] = cvt_pk_h(p0, p1);
+      lp = __builtin_amdgcn_fdot2(as_h2(pa[i]), as_h2(ones), lp, false);
+    }
+    l_run = __builtin_fmaf(l_run, alpha, lp);
+    m_run = mn;
+
+    // ---- V -> per-dim fp16 B operands, next chunk's V in flight, O += P V
+    uint32_t vlo[8], vhi[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      vlo[s] = vr[s][0];
+      vhi[s] = vr[s][1];
+      if constexpr (NORMQ) {
+        if (min(cpos(c) + vpos(s), L - 1) == pos_new) {
+          vlo[s] = reinterpret_cast<const uint32_t*>(vnew)[2 * col];
+          vhi[s] = reinterpret_cast<const uint32_t*>(vnew)[2 * col + 1];
         }
       }
-      dot_dpp_fence();
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        acc[g] += dpp<kDppQuadXor1>(acc[g]);
-        acc[g] += dpp<kDppQuadXor2>(acc[g]);
-      }
-      if (dq == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) sc[g][p] = (p < nt) ? acc[g] * sscale : -INFINITY;
-      }
     }
-    const int nb = base + TILE;  // next tile
-    if (nb < n) load_k(nb, min(TILE, n - nb));
-    __syncthreads();
+    uint32_t tr[8][2];  // tr[d][h]: dim 8col + d, bytes of k-slots 4h .. 4h+3
+    {
+      uint32_t x[4];
+      transpose4x4(vlo, x);
+      for (int d = 0; d < 4; ++d) tr[d][0] = x[d];
+      transpose4x4(vlo + 4, x);
+      for (int d = 0; d < 4; ++d) tr[d][1] = x[d];
+      transpose4x4(vhi, x);
+      for (int d = 0; d < 4; ++d) tr[4 + d][0] = x[d];
+      transpose4x4(vhi + 4, x);
+      for (int d = 0; d < 4; ++d) tr[4 + d][1] = x[d];
+    }
+    if (more) load_v(vr, c + 4);
+    if (rescale) {
+      float ar[4];  // alpha of the C rows' heads 4g + r (lane 4g + r holds that head)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r);
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[d][r] *= ar[r];
+    }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const u4_t vb = u4_t{fp8x2_h2<false>(tr[d][0]), fp8x2_h2<true>(tr[d][0]),
+                           fp8x2_h2<false>(tr[d][1]), fp8x2_h2<true>(tr[d][1])};
+      o[d] = mfma16(pa, vb, o[d]);
+    }
+  };
+  for (int c = wave; c < nchunk; c += 4) step(kr0, vr0, c);
 
-    // ---- online softmax: tile max, rescale of the running state, fp16
-    // probabilities of position pairs.  Lane j holds positions PPL*j ...
-    constexpr int PPL = TILE >= 256 ? 4 : 2;
-    const bool act = lane * PPL < TILE;
-    for (int g = wave; g < G; g += 4) {
-      float v[PPL];
-#pragma unroll
-      for (int i = 0; i < PPL; ++i) v[i] = act ? sc[g][PPL * lane + i] : -INFINITY;
-      float vm = v[0];
-#pragma unroll
-      for (int i = 1; i < PPL; ++i) vm = fmaxf(vm, v[i]);
-      const float mt = wave_max(vm);
-      const float mo = stat[g][0];
-      const float mn = fmaxf(mo, mt);
-      const float alpha = (mo == -INFINITY) ? 0.f : __expf(mo - mn);
-      float pr[PPL], ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < PPL; ++i) {
-        pr[i] = (mn == -INFINITY) ? 0.f : h2f(f2h(__expf(v[i] - mn)));
-        ps += pr[i];
-      }
-      const float l = wave_sum(ps);
-      if (act) {
-#pragma unroll
-        for (int j = 0; j < PPL / 2; ++j)
-          pp[g][(PPL / 2) * lane + j] =
-              (uint32_t)f2h(pr[2 * j]) | ((uint32_t)f2h(pr[2 * j + 1]) << 16);
-      }
-      if (lane == 0) {
-        stat[g][0] = mn;
-        stat[g][1] = __builtin_fmaf(stat[g][1], alpha, l);
-        stat[g][2] = alpha;
-      }
-    }
-    __syncthreads();
-
-    // ---- P V: lane d4 owns dims 4*d4 .. 4*d4+3 of position pairs
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float a = stat[g][2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[g][j] *= a;
-    }
-#pragma unroll
-    for (int k = 0; k < kPairs; ++k) {
-      const int i = 2 * wave + half + 8 * k;
-      uint32_t av = va[k], bv = vb[k];
-      if constexpr (NORMQ) {  // the new position: codes from this launch
-        const uint32_t nv = reinterpret_cast<const uint32_t*>(vnew)[d4];
-        if (s0 + base + min(2 * i, nt - 1) == pos_new) av = nv;
-        if (s0 + base + min(2 * i + 1, nt - 1) == pos_new) bv = nv;
-      }
-      // (a0 a1 c0 c1) and (a2 a3 c2 c3): decode gives (a_d, c_d) pairs per dim
-      const uint32_t x0 = __builtin_amdgcn_perm(bv, av, 0x05040100u);
-      const uint32_t x1 = __builtin_amdgcn_perm(bv, av, 0x07060302u);
-      uint32_t h0, h1, h2, h3;
-      fp8x4_to_h2_div256(x0, h0, h1);
-      fp8x4_to_h2_div256(x1, h2, h3);
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const h2_t pg = as_h2(pp[g][i]);
-        o[g][0] = __builtin_amdgcn_fdot2(as_h2(h0), pg, o[g][0], false);
-        o[g][1] = __builtin_amdgcn_fdot2(as_h2(h1), pg, o[g][1], false);
-        o[g][2] = __builtin_amdgcn_fdot2(as_h2(h2), pg, o[g][2], false);
-        o[g][3] = __builtin_amdgcn_fdot2(as_h2(h3), pg, o[g][3], false);
-      }
-    }
-    if (nb < n) load_v(nb, min(TILE, n - nb));
-    __syncthreads();  // sc / pp / stat rescale reused by the next tile
+  // ---- merge the 4 waves (each: max and sum per head, O rows per head)
+  float lsum = l_run + __shfl_xor(l_run, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if (g == 0 && col < G) {
+    wst[wave][col][0] = m_run;
+    wst[wave][col][1] = lsum;
   }
-
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * g + r;
+    if (h < G) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[2 * wave + half][d4][4 * g + j] = o[g][j];
+      for (int d = 0; d < 8; ++d) wo[wave][h][8 * col + d] = o[d][r];
+    }
+  }
   __syncthreads();
-
-  // ---- reduce over the 8 (wave, half) slots into ostage[G][128]
-  float* ostage = &sc[0][0];
-  const float oscale = vs * 256.0f;
+  const float oscale = vs;
   for (int e = t; e < G * 128; e += 256) {
-    const int g = e >> 7, d = e & 127;
-    float s = 0.f;
+    const int h = e >> 7, d = e & 127;
+    float M = wst[0][h][0];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) s += red[r][d >> 2][4 * g + (d & 3)];
-    ostage[e] = s * oscale;
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, wst[w][h][0]);
+    float acc = 0.f, l = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = wst[w][h][0];
+      const float ew = (mw == -INFINITY) ? 0.f : __expf(mw - M);
+      acc = __builtin_fmaf(ew, wo[w][h][d], acc);
+      l = __builtin_fmaf(ew, wst[w][h][1], l);
+    }
+    ostage[h][d] = acc * oscale;
+    if (d == 0) {
+      fin[h][0] = M;
+      fin[h][1] = l;
+    }
   }
   __syncthreads();
 
-  // ---- one thread per 32-dim chunk: FWHT-32 in registers (it is linear,
-  // so it commutes with the split merge), then either the final fp16 output
-  // (single split) or the fp32 partial (m, l, o).
+  // ---- one thread per 32-dim chunk: FWHT-32 (linear, so it commutes with
+  // the split merge), then the final fp16 output (single split) or the fp32
+  // partial (m, l, o)
   if (t < 4 * G) {
-    const int g = t >> 2, c = t & 3;
+    const int h = t >> 2, cq = t & 3;
     float v[32];
 #pragma unroll
     for (int i = 0; i < 32; i += 4) {
-      const f4_t x = *reinterpret_cast<const f4_t*>(&ostage[g * 128 + 32 * c + i]);
+      const f4_t x = *reinterpret_cast<const f4_t*>(&ostage[h][32 * cq + i]);
       v[i] = x[0];
       v[i + 1] = x[1];
       v[i + 2] = x[2];
@@ -365,9 +371,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     }
     if (fwht) fwht32(v);
     if (nsplit == 1) {
-      const float l = stat[g][1];
+      const float l = fin[h][1];
       const float inv = l > 0.f ? 1.0f / l : 0.f;
-      uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + g) * 128 + 32 * c;
+      uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + h) * 128 + 32 * cq;
 #pragma unroll
       for (int i = 0; i < 32; i += 8) {
         u4_t w;
@@ -377,15 +383,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
         *reinterpret_cast<u4_t*>(dst + i) = w;
       }
     } else {
-      float* dst = part + ((b * H + (int64_t)kh * G + g) * nsplit + sp) * kPart;
+      float* dst = part + ((b * H + (int64_t)kh * G + h) * nsplit + sp) * kPart;
 #pragma unroll
       for (int i = 0; i < 32; i += 4) {
         const f4_t x = {v[i], v[i + 1], v[i + 2], v[i + 3]};
-        *reinterpret_cast<f4_t*>(dst + 4 + 32 * c + i) = x;
+        *reinterpret_cast<f4_t*>(dst + 4 + 32 * cq + i) = x;
       }
-      if (c == 0) {
-        dst[0] = stat[g][0];
-        dst[1] = stat[g][1];
+      if (cq == 0) {
+        dst[0] = fin[h][0];
+        dst[1] = fin[h][1];
       }
     }
   }
@@ -439,18 +445,18 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
 
 int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
   // About 128 positions of the cache capacity per split, at most 64 splits
-  // (measured on MI355X at 2K-32K contexts, batch 1 and 8: more splits add
-  // merge traffic and per-workgroup fixed cost faster than they add
-  // parallelism).  Depends only on the cache capacity, so a captured graph
-  // stays valid as the sequence grows.
-  (void)B;
-  (void)Hk;
+  // and at most 512 workgroups (2 per CU at the kernel's register use);
+  // measured on MI355X with cold caches at 2K-32K contexts, batch 1 and 8.
+  // Depends only on the cache capacity, so a captured graph stays valid as
+  // the sequence grows.
   if (const char* e = getenv("R4Q_ATTN_SPLITS")) {  // tuning override
     const int v = atoi(e);
     if (v >= 1 && v <= kMaxSplits) return v;
   }
   int64_t n = (cap_len + 127) / 128;
   if (n > 64) n = 64;
+  const int64_t by_wg = 512 / (B * Hk > 0 ? B * Hk : 1);
+  if (n > by_wg) n = by_wg;
   return (int)(n < 1 ? 1 : n);
 }
 
@@ -472,33 +478,25 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
   const auto* vp = static_cast<const uint8_t*>(v_cache);
-  // tile: the shortest that holds the longest split this launch can see
-  const int64_t lmax = seq_len_dev ? max_seq : seq_len;
-  const int64_t smax = (lmax + nsplit - 1) / nsplit;
-  const int tile = smax <= 64 ? 64 : smax <= 128 ? 128 : 256;
-#define R4Q_ATTN(GG, TT)                                                                      \
-  if (G == GG && tile == TT) {                                                                \
+  bool launched = false;
+#define R4Q_ATTN_MFMA(GG)                                                                     \
+  if (!launched && G == GG) {                                                                 \
     if (qk)                                                                                   \
-      hipLaunchKernelGGL((attn_partial_kernel<GG, TT, true>), grid, dim3(256), 0, st, qp,       \
-                         q_stride, kp, vp, k_scale, v_scale, part,                            \
-                         static_cast<uint16_t*>(out), out_stride, fwht, (int)H, (int)Hk,      \
-                         (int)max_seq, (int)seq_len, seq_len_dev, nsplit, *qk);               \
+      hipLaunchKernelGGL((attn_mfma_kernel<GG, true>), grid, dim3(256), 0, st, qp, q_stride,   \
+                         kp, vp, k_scale, v_scale, part, static_cast<uint16_t*>(out),         \
+                         out_stride, fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len,       \
+                         seq_len_dev, nsplit, *qk);                                           \
     else                                                                                      \
-      hipLaunchKernelGGL((attn_partial_kernel<GG, TT, false>), grid, dim3(256), 0, st, qp,      \
-                         q_stride, kp, vp, k_scale, v_scale, part,                            \
-                         static_cast<uint16_t*>(out), out_stride, fwht, (int)H, (int)Hk,      \
-                         (int)max_seq, (int)seq_len, seq_len_dev, nsplit, AttnQK{});           \
+      hipLaunchKernelGGL((attn_mfma_kernel<GG, false>), grid, dim3(256), 0, st, qp, q_stride,  \
+                         kp, vp, k_scale, v_scale, part, static_cast<uint16_t*>(out),         \
+                         out_stride, fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len,       \
+                         seq_len_dev, nsplit, AttnQK{});                                      \
     launched = true;                                                                          \
   }
-  bool launched = false;
-  R4Q_ATTN(1, 64) R4Q_ATTN(1, 128) R4Q_ATTN(1, 256)
-  R4Q_ATTN(2, 64) R4Q_ATTN(2, 128) R4Q_ATTN(2, 256)
-  R4Q_ATTN(4, 64) R4Q_ATTN(4, 128) R4Q_ATTN(4, 256)
-  R4Q_ATTN(5, 64) R4Q_ATTN(5, 128) R4Q_ATTN(5, 256)
-  R4Q_ATTN(8, 64) R4Q_ATTN(8, 128) R4Q_ATTN(8, 256)
+  R4Q_ATTN_MFMA(1) R4Q_ATTN_MFMA(2) R4Q_ATTN_MFMA(4) R4Q_ATTN_MFMA(5) R4Q_ATTN_MFMA(8)
+#undef R4Q_ATTN_MFMA
   if (!launched)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
-#undef R4Q_ATTN
   if (nsplit > 1)
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)H, (unsigned)B), dim3(64), 0, st, part,
                        static_cast<uint16_t*>(out), out_stride, (int)H, nsplit);
