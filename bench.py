@@ -203,6 +203,64 @@ def read_floor(dev, iters=200, copies=8):
     return e0.elapsed_time(e1) * 1000.0 / (reps * iters), nbytes
 
 
+def flash_decode_leg(dev, ctx, iters=100):
+    """Config 2: r4q_flash_decode at batch 1, 40 query / 8 KV heads, cold KV.
+
+    A ring of KV cache pairs larger than 512 MB (more than the 256 MB
+    last-level cache) is cycled by `iters` launches captured in one hipGraph
+    on a private stream; HIP events on that stream give the average launch
+    (partials + split merge).  Returns (us, KV bytes per launch)."""
+    import ctypes as C
+
+    import torch
+
+    import r4q_lib as R
+    H, Hk, D = 40, 8, 128
+    max_seq = ctx + 64
+    kvb = Hk * max_seq * D
+    ncopy = max(2, min(64, (1 << 29) // (2 * kvb) + 1))
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    caches = []
+    for _ in range(ncopy):
+        # E4M3 codes of the encoder's range: |value| <= 1.75, no 0x7F / 0xFF
+        k = torch.randint(0, 0x40, (Hk, max_seq, D), dtype=torch.uint8, device=dev, generator=g)
+        k |= torch.randint(0, 2, (Hk, max_seq, D), dtype=torch.uint8, device=dev, generator=g) << 7
+        v = torch.randint(0, 0x40, (Hk, max_seq, D), dtype=torch.uint8, device=dev, generator=g)
+        caches.append((k, v))
+    q = torch.randn(H * D, device=dev, generator=g).half()
+    out = torch.empty(H * D, dtype=torch.float16, device=dev)
+    ctx_h = C.c_void_p()
+    R.call("r4q_ctx_create", C.byref(ctx_h))
+    st = torch.cuda.Stream(dev)
+
+    def launch(i):
+        k, v = caches[i % ncopy]
+        R.call("r4q_flash_decode", ctx_h, q.data_ptr(), H * D, k.data_ptr(), v.data_ptr(), None,
+               None, out.data_ptr(), 1, H, Hk, D, max_seq, ctx, 1, st.cuda_stream)
+
+    launch(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        for i in range(iters):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = 3
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    with torch.cuda.stream(st):
+        for _ in range(reps):
+            graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+    del graph
+    R.call("r4q_ctx_destroy", ctx_h)
+    return us, Hk * ctx * 2 * D
+
+
 def copy_calibration(dev, mib=256, iters=20):
     """A plain copy of known size (fp16 negation: `mib` MiB read, `mib` MiB
     written per launch) whose FETCH_SIZE / WRITE_SIZE counters calibrate the
@@ -294,6 +352,15 @@ def main():
     rf_us, rf_bytes = read_floor(dev)
     log(f"INT4 GEMV 5120->17408: {us:.2f} us, {gbps:.0f} GB/s; plain read of its "
         f"{rf_bytes} bytes: {rf_us:.2f} us")
+
+    attn = {}
+    for c in (2048, 8192, 32768):
+        a_us, a_bytes = flash_decode_leg(dev, c)
+        attn[str(c)] = {"us": round(a_us, 3), "kv_bytes": a_bytes,
+                        "gbps": round(a_bytes / a_us / 1e3, 1),
+                        "frac": round(a_bytes / a_us / 1e3 / HBM_PEAK_GBPS, 4)}
+        log(f"flash-decode ctx={c}: {a_us:.2f} us, {a_bytes / a_us / 1e3:.0f} GB/s (cold KV)")
+    torch.cuda.empty_cache()
 
     log("building synthetic model")
     t0 = time.time()
@@ -389,6 +456,8 @@ def main():
             "read_floor_us": round(rf_us, 3),
             "frac_of_read_floor": round(rf_us / us, 4),
         },
+        # config 2: flash-decode alone, batch 1, cold KV (ring > 512 MB), per ctx
+        "flash_decode": attn,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
