@@ -9,7 +9,7 @@ import torch
 import r4q_lib as R
 import r4q_oracle as O
 import r4q_synth as S
-from conftest import rel_l2
+from conftest import fp8_golden_table, rel_l2
 
 pytestmark = pytest.mark.gpu
 TOL = 5e-3
@@ -68,6 +68,33 @@ def test_flash_decode_single_position_is_v(dev, ctx):
     """seq_len 1: softmax weight 1, output equals the (scaled) V row."""
     got = _case(dev, ctx, 1, 40, 8, 1, 4, scaled=True, fwht=False, seed=5)
     assert np.all(np.isfinite(got))
+
+
+def test_flash_decode_widens_every_encoder_code_exactly(dev, ctx):
+    """With one position the softmax weight is exactly 1, so the unrotated
+    output is fp16(decoded V) bit for bit.  Every E4M3 code except the
+    subnormals (0x01-0x07, 0x81-0x87) and 0x7F / 0xFF must widen to the
+    reference decoder's value (hip:71-81); the golden encoder table shows
+    the reference encoder never emits those excluded codes."""
+    excluded = {c for c in range(256) if (c & 0x7F) == 0x7F or ((c >> 3) & 0xF == 0 and c & 7)}
+    assert not excluded & set(np.unique(fp8_golden_table()).tolist())
+    codes = np.array([c for c in range(256) if c not in excluded], np.uint8)
+    want = O.fp8_decode_ref(codes).astype(np.float16)
+    q = torch.ones(128, dtype=torch.float16, device=dev)
+    out = torch.empty(128, dtype=torch.float16, device=dev)
+    kc = torch.zeros(1, 1, 1, 128, dtype=torch.uint8, device=dev)
+    for c0 in range(0, codes.size, 128):
+        part = codes[c0:c0 + 128]
+        row = np.zeros(128, np.uint8)
+        row[:part.size] = part
+        vc = torch.from_numpy(row.reshape(1, 1, 1, 128)).to(dev)
+        R.call("r4q_flash_decode", ctx, q.data_ptr(), 128, kc.data_ptr(), vc.data_ptr(), None,
+               None, out.data_ptr(), 1, 1, 1, 128, 1, 1, 0, R.stream_handle())
+        got = out.cpu().numpy()[:part.size]
+        w = want[c0:c0 + part.size]
+        # -0 sums to +0 in the fp32 accumulation: values everywhere, bits off zero
+        assert np.array_equal(got, w), c0
+        assert np.array_equal(got[w != 0].view(np.uint16), w[w != 0].view(np.uint16)), c0
 
 
 def test_flash_decode_rejects_bad_arguments(dev, ctx):
