@@ -47,6 +47,8 @@
  *                           and decode_loop (:3284-3466) via tokens_out
  *   r4q_decode_profile   <- decode_profile          (:3047-3273)
  *   r4q_prefill_logits   <- prefill_logits          (:2127-2320)
+ *   r4q_decode_generate, r4q_sample <- the Python sampling of the engine
+ *                           (int4_engine_v5.py:330-335, 387-399)
  */
 #ifndef R4Q_H
 #define R4Q_H
@@ -241,6 +243,25 @@ R4Q_API int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden
 R4Q_API int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                      int64_t B, int64_t num_tokens, int64_t start_pos,
                      int use_graph, void* tokens_out, void* stream);
+/* r4q_decode_bench with temperature / top-p sampling of each next token on
+ * the device (the reference samples in Python, int4_engine_v5.py:387-399):
+ * temperature > 0 draws from softmax(logits / temperature) restricted to
+ * the tokens whose cumulative probability before them (descending order,
+ * ties by index) is < top_p (top_p >= 1 keeps all); the uniform draw of row
+ * b at position pos is splitmix64(splitmix64(seed ^ pos) ^ b) >> 40 / 2^24.
+ * temperature == 0 is the greedy loop of r4q_decode_bench. */
+R4Q_API int r4q_decode_generate(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                                int64_t B, int64_t num_tokens, int64_t start_pos,
+                                int use_graph, float temperature, float top_p, uint64_t seed,
+                                void* tokens_out, void* stream);
+/* Next token of each of B rows of fp16 logits [B, row_stride] (first V used)
+ * with the rule of r4q_decode_generate, `counter` in place of the position;
+ * temperature <= 0 is argmax (lowest index of the maximum).  Replaces the
+ * reference's Python sampling (int4_engine_v5.py:330-335, 387-399);
+ * ids_out: int64 [B] on the device.  Logits must not be NaN. */
+R4Q_API int r4q_sample(r4q_ctx* ctx, const void* logits, int64_t B, int64_t V, int64_t row_stride,
+                       float temperature, float top_p, uint64_t seed, int64_t counter,
+                       int64_t* ids_out, void* stream);
 /* Time one step by kernel category with HIP events:
  * out_ms[5] = {total, gemv, attention, norm, rest}. */
 R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,

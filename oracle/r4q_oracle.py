@@ -52,6 +52,11 @@ PINNING = {
                          "enable_gqa=True) (hip:2262-2264); M=1 closed form (= v)",
     "prefill_logits": "composition of the pinned functions; row m of the prompt pass "
                       "equals the decode step at position m on the same caches",
+    "sample_top_p": "kept set vs a literal torch restatement of the reference's top-p "
+                    "code (int4_engine_v5.py:387-399: sort, cumsum, mask) in float64; "
+                    "draw frequencies vs the renormalised kept distribution "
+                    "(chi-square); temperature 0 == torch.argmax; splitmix64 against "
+                    "its published test vector",
 }
 
 INV_SQRT32 = np.float32(0.17677669529663689)
@@ -534,3 +539,87 @@ def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos
     if final_norm is not None:
         logits = gemm(rot, lm_w, lm_s, lm_bits)
     return x, logits
+
+
+# ------------------------------------------------------- f3 sampling
+_M64 = (1 << 64) - 1
+
+
+def splitmix64(x: int) -> int:
+    """splitmix64 output function (S. Vigna): one step from state x."""
+    x = (x + 0x9E3779B97F4A7C15) & _M64
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & _M64
+    return x ^ (x >> 31)
+
+
+def sample_uniform(seed: int, counter: int, row: int) -> np.float32:
+    """The draw's uniform u in [0, 1): splitmix64(splitmix64(seed ^ counter)
+    ^ row), top 24 bits / 2^24 (the library's counter-based stream)."""
+    x = splitmix64(splitmix64((seed ^ (counter & _M64)) & _M64) ^ row)
+    return np.float32((x >> 40) / 16777216.0)
+
+
+def sample_top_p(logits16, temperature: float, top_p: float, u: float,
+                 return_info: bool = False):
+    """Next token of one row (int4_engine_v5.py:387-399): z = float(logits) /
+    temperature; with top_p < 1 the tokens are sorted by z descending (ties
+    by ascending index, a stable sort) and a token is dropped when the
+    softmax mass before it is >= top_p; one token is drawn from the kept
+    tokens' softmax by inverse CDF at u in that same order.  temperature <= 0
+    is argmax (the lowest index of the maximum, int4_engine_v5.py:352-353).
+
+    return_info adds the cutoff margin (distance of the nearest cumulative
+    mass to top_p) and the draw margin (distance of u * kept mass to the
+    nearest CDF step), in probability units, so tests can skip cases whose
+    outcome hinges on float rounding."""
+    l = np.asarray(logits16, dtype=np.float16).astype(np.float32).ravel()
+    V = l.size
+    if temperature <= 0:
+        tok = int(np.argmax(l))
+        info = {"cut_margin": np.inf, "draw_margin": np.inf, "token": tok}
+        return (tok, info) if return_info else tok
+    z = (l / np.float32(temperature)).astype(np.float32)
+    order = np.lexsort((np.arange(V), -z.astype(np.float64)))
+    zs = z[order].astype(np.float64)
+    p = np.exp(zs - zs[0])
+    p /= p.sum()
+    before = np.cumsum(p) - p
+    if top_p < 1.0:
+        keep = before < top_p
+        cut_margin = float(np.min(np.abs(before - top_p)))
+    else:
+        keep = np.ones(V, bool)
+        cut_margin = np.inf
+    pk = p[keep]
+    cdf = np.cumsum(pk)
+    target = float(u) * cdf[-1]
+    j = int(np.searchsorted(cdf, target, side="right"))
+    j = min(j, pk.size - 1)
+    tok = int(order[np.flatnonzero(keep)[j]])
+    if not return_info:
+        return tok
+    steps = np.concatenate([[0.0], cdf])
+    draw_margin = float(np.min(np.abs(steps - target)))
+    return tok, {"cut_margin": cut_margin, "draw_margin": draw_margin,
+                 "kept": int(keep.sum()), "order": order, "before": before, "keep": keep,
+                 "cdf": cdf / cdf[-1], "u": float(u), "top_p": top_p}
+
+
+def sample_distance(token: int, info) -> float:
+    """How far (probability units) a token chosen by another implementation
+    lies from the oracle's outcome: 0 for the oracle's own token; for another
+    kept token, the distance of u to that token's CDF interval; for a
+    dropped token, the distance of its cumulative mass before it to top_p (a
+    cutoff decided by rounding)."""
+    if "order" not in info:  # greedy: no rounding-dependent outcome
+        return 0.0 if token == info["token"] else np.inf
+    pos = int(np.flatnonzero(info["order"] == token)[0])
+    if not info["keep"][pos]:
+        return float(abs(info["before"][pos] - info["top_p"]))
+    j = int(np.flatnonzero(np.flatnonzero(info["keep"]) == pos)[0])
+    lo = 0.0 if j == 0 else float(info["cdf"][j - 1])
+    hi = float(info["cdf"][j])
+    u = info["u"]
+    return max(0.0, lo - u, u - hi)
+

@@ -27,6 +27,8 @@ struct r4q_ctx {
   r4q::DevBuf step;      // decode-step activations
   r4q::DevBuf prefill;   // prefill activations
   r4q::DevBuf misc;      // device-side position / counters
+  r4q::DevBuf sample;    // sampling tables (kept zeroed between calls)
+  size_t sample_zeroed = 0;  // bytes of `sample` known to be zero
   r4q::GraphCache* graphs = nullptr;
 };
 
@@ -35,10 +37,12 @@ namespace r4q {
 // Flash-decode internals used by the decode step.
 // Chooses the split count for `seq_len` positions over B*Hk heads.
 int attn_num_splits(int64_t seq_len, int64_t B, int64_t Hk);
+// Sampling workspace for B rows, zeroed on (re)allocation.
+int sample_reserve(r4q_ctx* ctx, int64_t B, hipStream_t st, void** ws);
 // Bytes of partial-result scratch for a launch.
 size_t attn_ws_bytes(int64_t B, int64_t H, int nsplit);
 // Enqueues partial + combine; seq_len_dev != nullptr: length read on device
-// (nsplit must then cover the largest length: seq_len <= 256 * nsplit).
+// (any length up to max_seq; nsplit is chosen from the capacity).
 // Fused decode-step prologue (NORMQ): q of the workgroup's query heads and
 // the new position's K/V come raw from the QKV projection row; the
 // workgroup applies the head RMSNorm + RoPE (head_norm_rope_pair, the

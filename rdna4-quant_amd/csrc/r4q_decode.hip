@@ -46,9 +46,6 @@ void destroy_graphs(r4q_ctx* ctx) {
 
 namespace {
 
-// Device state words (ctx->misc): position, sequence length, step counter.
-enum { kPos = 0, kSeq = 1, kStep = 2, kStateWords = 4 };
-
 struct Dims {
   int L, H, Hk, hd, D, I, qkvN, qd;
   float eps;
@@ -326,8 +323,25 @@ __global__ void advance_kernel(int* state) {
   state[kStep] += 1;
 }
 
+// Next token of every row from bf.logits: greedy argmax, or temperature /
+// top-p sampling when `scfg` has temperature > 0 (draw counter = the step's
+// position: state[kPos] on the device, else pos_host); then its embedding
+// into bf.h and, in a captured loop, the position advance.
 int enqueue_sample(const r4q_model* m, const Dims& dm, int64_t B, const Bufs& bf,
-                   int64_t* tokens_out, bool device_step, int step_host, hipStream_t st) {
+                   int64_t* tokens_out, bool device_step, int step_host, hipStream_t st,
+                   const SampleCfg* scfg = nullptr, void* sample_ws = nullptr,
+                   int64_t pos_host = 0) {
+  if (scfg && scfg->temperature > 0.f) {
+    R4Q_TRY(launch_sample(bf.logits, B, m->lm_N, m->lm_N, *scfg,
+                          device_step ? bf.state + kPos : nullptr, pos_host, sample_ws, bf.ids,
+                          m->embed, dm.D, bf.h, tokens_out, device_step ? bf.state : nullptr,
+                          step_host, st));
+    if (device_step) {
+      hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, bf.state);
+      R4Q_TRY(launch_status("advance"));
+    }
+    return R4Q_OK;
+  }
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, (unsigned)B), dim3(256), 0, st,
                      bf.logits, m->lm_N, bf.amax);
   R4Q_TRY(launch_status("argmax"));
@@ -355,8 +369,9 @@ int check_positions(const r4q_model* m, int64_t first, int64_t count) {
 
 // Key of a captured graph: model struct, layer table and launch shape.
 std::vector<uint8_t> graph_key(const r4q_model* m, int64_t B, int nsplit, const void* tokens_out,
-                               const Bufs& bf) {
-  std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 64);
+                               const Bufs& bf, const SampleCfg& scfg) {
+  std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 64 +
+                         sizeof(SampleCfg));
   uint8_t* p = k.data();
   memcpy(p, m, sizeof(r4q_model));
   p += sizeof(r4q_model);
@@ -366,6 +381,7 @@ std::vector<uint8_t> graph_key(const r4q_model* m, int64_t B, int nsplit, const 
   memcpy(p, &B, 8);
   memcpy(p + 8, &nsplit, 4);
   memcpy(p + 16, extra, sizeof(extra));
+  memcpy(p + 16 + sizeof(extra), &scfg, sizeof(SampleCfg));
   return k;
 }
 
@@ -395,9 +411,14 @@ extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hid
   return R4Q_OK;
 }
 
-extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
-                                int64_t num_tokens, int64_t start_pos, int use_graph,
-                                void* tokens_out, void* stream) {
+namespace r4q {
+namespace {
+// The decode loop behind r4q_decode_bench (greedy) and r4q_decode_generate
+// (temperature / top-p): num_tokens steps from start_pos, next token and its
+// embedding on the device between steps, optionally captured in a hipGraph.
+int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
+                int64_t num_tokens, int64_t start_pos, int use_graph, void* tokens_out,
+                const SampleCfg& scfg, void* stream) {
   R4Q_REQUIRE(ctx && hidden_in, "decode_bench: null context or input");
   Dims dm;
   R4Q_TRY(validate(m, B, dm));
@@ -410,12 +431,14 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
   R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
   int64_t* toks = static_cast<int64_t*>(tokens_out);
+  void* sws = nullptr;
+  if (scfg.temperature > 0.f) R4Q_TRY(sample_reserve(ctx, B, st, &sws));
   R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
   if (!use_graph) {
     for (int64_t t = 0; t < num_tokens; ++t) {
       const int64_t pos = start_pos + t;
       R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, true, st));
-      R4Q_TRY(enqueue_sample(m, dm, B, bf, toks, false, (int)t, st));
+      R4Q_TRY(enqueue_sample(m, dm, B, bf, toks, false, (int)t, st, &scfg, sws, pos));
     }
     return R4Q_OK;
   }
@@ -429,7 +452,7 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
   (void)hipStreamWaitEvent(gc.stream, ev, 0);
   hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, gc.stream, bf.state, (int)start_pos);
   int rc = launch_status("set_state");
-  std::vector<uint8_t> key = graph_key(m, B, nsplit, tokens_out, bf);
+  std::vector<uint8_t> key = graph_key(m, B, nsplit, tokens_out, bf, scfg);
   if (rc == R4Q_OK && (!gc.exec || gc.key != key)) {
     if (gc.exec) {
       (void)hipGraphExecDestroy(gc.exec);
@@ -443,7 +466,7 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
       const int* pos_dev = bf.state + kPos;
       const int* seq_dev = bf.state + kSeq;
       int rc1 = enqueue_step(m, dm, B, start_pos, pos_dev, seq_dev, nsplit, bf, true, gc.stream);
-      if (rc1 == R4Q_OK) rc1 = enqueue_sample(m, dm, B, bf, toks, true, 0, gc.stream);
+      if (rc1 == R4Q_OK) rc1 = enqueue_sample(m, dm, B, bf, toks, true, 0, gc.stream, &scfg, sws);
       e = hipStreamEndCapture(gc.stream, &graph);
       if (rc1 != R4Q_OK) rc = rc1;
       else if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
@@ -467,6 +490,25 @@ extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hi
   (void)hipStreamWaitEvent(st, ev, 0);
   (void)hipEventDestroy(ev);
   return rc;
+}
+}  // namespace
+}  // namespace r4q
+
+extern "C" int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
+                                int64_t num_tokens, int64_t start_pos, int use_graph,
+                                void* tokens_out, void* stream) {
+  return r4q::decode_loop(ctx, m, hidden_in, B, num_tokens, start_pos, use_graph, tokens_out,
+                          r4q::SampleCfg{0.f, 1.f, 0}, stream);
+}
+
+extern "C" int r4q_decode_generate(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                                   int64_t B, int64_t num_tokens, int64_t start_pos,
+                                   int use_graph, float temperature, float top_p, uint64_t seed,
+                                   void* tokens_out, void* stream) {
+  R4Q_REQUIRE(temperature >= 0.f && top_p > 0.f,
+              "decode_generate: need temperature >= 0 and top_p > 0");
+  return r4q::decode_loop(ctx, m, hidden_in, B, num_tokens, start_pos, use_graph, tokens_out,
+                          r4q::SampleCfg{temperature, top_p, seed}, stream);
 }
 
 extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,

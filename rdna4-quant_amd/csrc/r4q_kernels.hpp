@@ -26,6 +26,29 @@ int launch_head_norm_rope_kv(const void* qkv, int64_t qkv_stride, const void* qw
                              int64_t max_seq, int64_t pos, const int* pos_dev, hipStream_t st,
                              bool prefill_rows = false);
 
+// Device-side state of a captured decode loop (int words): the position
+// being decoded, the sequence length seen by attention, the step index.
+enum { kPos = 0, kSeq = 1, kStep = 2, kStateWords = 4 };
+
+// Temperature / top-p sampling (temperature > 0, 0 < top_p; top_p >= 1 keeps
+// every token), uniform draw from (seed, counter, row).
+struct SampleCfg {
+  float temperature;
+  float top_p;
+  uint64_t seed;
+};
+// Workspace for B <= 1024 rows: the selection words, then a zeroed
+// 65,536-bin table per row (left zeroed by every call; see sample_reserve).
+size_t sample_ws_bytes(int64_t B);
+// ids[b] = sampled token of row b of logits [B, stride] fp16 (V used).
+// counter_dev (device int) overrides counter_host.  With embed != nullptr
+// the token's embedding row goes to h[b] and tokens_out[step * B + b] = id
+// (step from state[kStep] when state != nullptr, else step_host).
+int launch_sample(const void* logits, int64_t B, int64_t V, int64_t stride, const SampleCfg& cfg,
+                  const int* counter_dev, int64_t counter_host, void* ws, int64_t* ids,
+                  const void* embed, int64_t D, void* h, int64_t* tokens_out, const int* state,
+                  int step_host, hipStream_t st);
+
 // out[m] = table[ids[m]] for M rows of D fp16 (ids already range-checked).
 int launch_embed_gather(const int64_t* ids, const void* table, void* out, int64_t M, int64_t D,
                         hipStream_t st);

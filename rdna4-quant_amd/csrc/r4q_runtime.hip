@@ -54,6 +54,7 @@ extern "C" int r4q_ctx_destroy(r4q_ctx* ctx) {
   ctx->step.release();
   ctx->prefill.release();
   ctx->misc.release();
+  ctx->sample.release();
   delete ctx;
   return R4Q_OK;
 }

@@ -352,7 +352,7 @@ def decode_step_logits(hidden_in, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s
 
 
 def _bench(hidden_in, embed_weight, num_tokens, rest, use_graph, tokens_out=None,
-           kv_scales=None):
+           kv_scales=None, temperature=0.0, top_p=1.0, seed=0):
     (qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N, in_norm_w,
      post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, start_pos, num_heads, num_kv_heads,
      head_dim, hidden_size, intermediate_size, rms_eps, k_caches, v_caches, final_norm_w, lm_w,
@@ -363,9 +363,14 @@ def _bench(hidden_in, embed_weight, num_tokens, rest, use_graph, tokens_out=None
     m, B, pos = _decode_common(hidden_in, la, k_caches, v_caches,
                                final=(final_norm_w, lm_w, lm_s, lm_N, lm_K), embed=embed_weight,
                                kv_scales=kv_scales)
-    _R.call("r4q_decode_bench", _context(), C.byref(m.struct), hidden_in.data_ptr(), B,
-            int(num_tokens), pos, 1 if use_graph else 0,
-            None if tokens_out is None else tokens_out.data_ptr(), _stream())
+    toks = None if tokens_out is None else tokens_out.data_ptr()
+    if temperature > 0:
+        _R.call("r4q_decode_generate", _context(), C.byref(m.struct), hidden_in.data_ptr(), B,
+                int(num_tokens), pos, 1 if use_graph else 0, float(temperature), float(top_p),
+                int(seed) & (2 ** 64 - 1), toks, _stream())
+    else:
+        _R.call("r4q_decode_bench", _context(), C.byref(m.struct), hidden_in.data_ptr(), B,
+                int(num_tokens), pos, 1 if use_graph else 0, toks, _stream())
 
 
 def decode_bench(hidden_in, embed_weight, num_tokens, *rest, kv_scales=None):
@@ -384,19 +389,44 @@ def decode_loop(embed_weight, final_norm_w, lm_w, lm_s, lm_N, lm_K, first_token_
                 qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N,
                 in_norm_w, post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, start_pos,
                 num_heads, num_kv_heads, head_dim, hidden_size, intermediate_size, rms_eps,
-                k_caches, v_caches, hadamard_mat, *, kv_scales=None):
-    """Greedy decode of num_tokens tokens; returns the token ids as a CPU
-    int64 tensor [num_tokens] (hip:3284-3466)."""
+                k_caches, v_caches, hadamard_mat, *, kv_scales=None, temperature=0.0,
+                top_p=1.0, seed=0, use_graph=False):
+    """Decode of num_tokens tokens with the next token chosen on the device;
+    returns the token ids as a CPU int64 tensor [num_tokens] (hip:3284-3466).
+    Greedy by default, as in the reference; temperature > 0 samples with
+    top_p on the device (the engine's Python sampling,
+    int4_engine_v5.py:387-399) from the counter-based stream of `seed` (see
+    `sample`).  use_graph=True replays one captured step per token."""
     B = first_token_hidden.numel() // hidden_size
     toks = torch.empty((int(num_tokens), B), dtype=torch.int64, device=first_token_hidden.device)
     rest = (qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N,
             in_norm_w, post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, start_pos, num_heads,
             num_kv_heads, head_dim, hidden_size, intermediate_size, rms_eps, k_caches, v_caches,
             final_norm_w, lm_w, lm_s, lm_N, lm_K, hadamard_mat)
-    _bench(first_token_hidden, embed_weight, num_tokens, rest, False, tokens_out=toks,
-           kv_scales=kv_scales)
+    _bench(first_token_hidden, embed_weight, num_tokens, rest, use_graph, tokens_out=toks,
+           kv_scales=kv_scales, temperature=temperature, top_p=top_p, seed=seed)
     out = toks.to("cpu")
     return out[:, 0] if B == 1 else out
+
+
+def sample(logits, temperature=0.0, top_p=1.0, seed=0, counter=0):
+    """Next token id of each row of fp16 logits [..., V] on the device, as an
+    int64 tensor of the leading shape -- the engine's Python sampling
+    (int4_engine_v5.py:330-335, 387-399) without the host round trip:
+    temperature <= 0 is argmax (lowest index of the maximum); otherwise a
+    draw from softmax(logits / temperature) over the tokens whose cumulative
+    probability before them (descending, ties by index) is < top_p, with the
+    uniform of row b taken from splitmix64(splitmix64(seed ^ counter) ^ b)."""
+    _need(logits.is_cuda and logits.dtype == torch.float16, "logits must be cuda float16")
+    V = logits.shape[-1]
+    rows = logits.reshape(-1, V)
+    if rows.stride(-1) != 1 or rows.stride(0) < V:
+        rows = rows.contiguous()
+    out = torch.empty(rows.shape[0], dtype=torch.int64, device=logits.device)
+    _R.call("r4q_sample", _context(), rows.data_ptr(), rows.shape[0], V, rows.stride(0),
+            float(temperature), float(top_p), int(seed) & (2 ** 64 - 1), int(counter),
+            out.data_ptr(), _stream())
+    return out.reshape(logits.shape[:-1])
 
 
 def decode_profile(hidden_in, embed_weight, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N,

@@ -86,6 +86,9 @@ SIGNATURES = {
                          _i64, C.c_int, _p],
     "r4q_decode_step": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _p, _p, _p],
     "r4q_decode_bench": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _i64, C.c_int, _p, _p],
+    "r4q_decode_generate": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _i64, C.c_int, _f32, _f32,
+                            C.c_uint64, _p, _p],
+    "r4q_sample": [_p, _p, _i64, _i64, _i64, _f32, _f32, C.c_uint64, _i64, _p, _p],
     "r4q_decode_profile": [_p, C.POINTER(R4QModel), _p, _i64, _fp, _p],
     "r4q_prefill_logits": [_p, C.POINTER(R4QModel), _p, _i64, _p, C.c_int, _p],
 }
