@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 
   // local chunk c: K rows cpos(c) + 16bb + col (32 bytes from dim 32g), V
   // rows cpos(c) + vpos(s) (8 bytes from dim 8col); rows past the sequence
-  // end are clamped to its last row and masked.  Only called for c < nchunk.
+  // end are clamped to its last row and masked.
   auto vpos = [&](int s) { return s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4); };
   // One register set per wave: the next chunk's K (V) loads are issued as
   // soon as this chunk's K (V) registers are converted (a second set in
@@ -143,33 +143,68 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
           reinterpret_cast<const u2_t*>(vbase + (p * 128u + 8u * col)));
     }
   };
-  if (wave < nchunk) {  // first chunk in flight during the query prologue
-    load_k(kr0, wave);
-    load_v(vr0, wave);
-  }
-
   // ---- query: B operands qb[j] = Q[head col][32g + 8j .. +7] (0 for col >= G)
+  // NORMQ: tasks 0 .. G-1 are the query heads, G the new K row and G+1 the
+  // new V row (the last two only in the workgroup holding position L-1);
+  // wave w takes tasks w, w+4, ...  Every prologue input is loaded before
+  // the wave's first KV chunk, so that the norm and RoPE run while the chunk
+  // is in flight (loads return in issue order).
+  constexpr int kSlots = (G + 2 + 3) / 4;
+  const int pos = L - 1;
+  const bool owner = NORMQ && (pos >> 5) % nsplit == sp;  // holds the new position's chunk
+  const int ntask = G + (owner ? 2 : 0);
+  uint16_t px[kSlots][2], pw[kSlots][2];  // raw fp16, widened after the KV loads issue
+  uint16_t pc = 0, ps = 0;
+  if constexpr (NORMQ) {
+    const uint16_t* row = q + b * q_stride;  // raw QKV row: q | k | v heads
+    // branch-free, so that all of them are in flight together (slots past
+    // the wave's tasks read head 0 and are not used)
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int task = wave + 4 * i;
+      const int head = task >= ntask ? 0 : task < G ? kh * G + task : task == G ? H + kh : H + Hk + kh;
+      const uint16_t* src = row + (int64_t)head * 128;
+      const uint16_t* w = task < G ? qk.qw : qk.kw;
+      px[i][0] = src[lane];
+      px[i][1] = src[lane + 64];
+      pw[i][0] = w[lane];
+      pw[i][1] = w[lane + 64];
+    }
+    pc = qk.cs[(int64_t)pos * 64 + lane];
+    ps = qk.sn[(int64_t)pos * 64 + lane];
+  }
+  // first chunk in flight during the query prologue; unconditional (a wave
+  // without chunks reads the clamped last row) so that the prologue waits
+  // only for its own, earlier loads
+  load_k(kr0, wave);
+  load_v(vr0, wave);
+
   u4_t qb[4];
   if constexpr (NORMQ) {
-    const int pos = L - 1;
-    const bool owner = (pos >> 5) % nsplit == sp;  // holds the new position's chunk
-    const uint16_t* row = q + b * q_stride;  // raw QKV row: q | k | v heads
-    const float c = h2f_ieee(qk.cs[(int64_t)pos * 64 + lane]);
-    const float sn = h2f_ieee(qk.sn[(int64_t)pos * 64 + lane]);
-    const int ntask = G + (owner ? 2 : 0);
-    for (int task = wave; task < ntask; task += 4) {
+    // widened in straight-line code: every slot's loads are consumed here,
+    // before any branch (none is sunk behind the KV loads)
+    const float c = h2f_ieee(pc), sn = h2f_ieee(ps);
+    float fx[kSlots][2], fw[kSlots][2];
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      fx[i][0] = h2f_ieee(px[i][0]);
+      fx[i][1] = h2f_ieee(px[i][1]);
+      fw[i][0] = h2f_ieee(pw[i][0]);
+      fw[i][1] = h2f_ieee(pw[i][1]);
+    }
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      const int task = wave + 4 * i;
+      if (task >= ntask) break;  // wave-uniform
+      const float x0 = fx[i][0], x1 = fx[i][1];
       if (task < G) {
-        const uint16_t* src = row + (int64_t)(kh * G + task) * 128;
         float lo, hi;
-        head_norm_rope_pair(h2f_ieee(src[lane]), h2f_ieee(src[lane + 64]), h2f_ieee(qk.qw[lane]),
-                            h2f_ieee(qk.qw[lane + 64]), c, sn, qk.eps, lo, hi);
+        head_norm_rope_pair(x0, x1, fw[i][0], fw[i][1], c, sn, qk.eps, lo, hi);
         qs[task][lane] = f2h(lo);
         qs[task][lane + 64] = f2h(hi);
       } else if (task == G) {
-        const uint16_t* src = row + (int64_t)(H + kh) * 128;
         float lo, hi;
-        head_norm_rope_pair(h2f_ieee(src[lane]), h2f_ieee(src[lane + 64]), h2f_ieee(qk.kw[lane]),
-                            h2f_ieee(qk.kw[lane + 64]), c, sn, qk.eps, lo, hi);
+        head_norm_rope_pair(x0, x1, fw[i][0], fw[i][1], c, sn, qk.eps, lo, hi);
         const float inv = ksc ? 1.0f / ksc[kh] : 1.0f;
         const uint8_t c0 = (uint8_t)fp8_encode(lo * inv), c1 = (uint8_t)fp8_encode(hi * inv);
         uint8_t* kp = qk.kc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
@@ -178,10 +213,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         knew[lane] = c0;
         knew[lane + 64] = c1;
       } else {
-        const uint16_t* src = row + (int64_t)(H + Hk + kh) * 128;
         const float inv = vsc ? 1.0f / vsc[kh] : 1.0f;
-        const uint8_t c0 = (uint8_t)fp8_encode(h2f_ieee(src[lane]) * inv);
-        const uint8_t c1 = (uint8_t)fp8_encode(h2f_ieee(src[lane + 64]) * inv);
+        const uint8_t c0 = (uint8_t)fp8_encode(x0 * inv);
+        const uint8_t c1 = (uint8_t)fp8_encode(x1 * inv);
         uint8_t* vp = qk.vc + ((b * Hk + kh) * (int64_t)max_seq + pos) * 128;
         vp[lane] = c0;
         vp[lane + 64] = c1;

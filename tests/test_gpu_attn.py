@@ -64,6 +64,16 @@ def test_flash_decode_batch8_no_rotation(dev, ctx):
     _case(dev, ctx, 8, 40, 8, 700, 1024, scaled=False, fwht=False, seed=8)
 
 
+@pytest.mark.parametrize("L", [257, 8192])
+def test_flash_decode_forced_split_counts(dev, ctx, monkeypatch, L):
+    """Split counts from 1 to 128 back to back on one context: more than one
+    64-split merge round, and splits that hold no positions when there are
+    fewer 32-position chunks than splits."""
+    for n in (3, 100, 1, 17, 128, 64, 2):
+        monkeypatch.setenv("R4Q_ATTN_SPLITS", str(n))
+        _case(dev, ctx, 2, 40, 8, L, L + 1, scaled=True, fwht=True, seed=n + L)
+
+
 def test_flash_decode_single_position_is_v(dev, ctx):
     """seq_len 1: softmax weight 1, output equals the (scaled) V row."""
     got = _case(dev, ctx, 1, 40, 8, 1, 4, scaled=True, fwht=False, seed=5)
