@@ -104,6 +104,17 @@ R4Q_API int r4q_gemv(const void* x, const void* w, const void* sz, void* y,
  * on the fly into an MFMA GEMM. */
 R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
              int64_t M, int64_t N, int64_t K, int wbits, void* stream);
+/* Device workspace (bytes, written to *bytes; 0: none) that lets r4q_gemm_ws
+ * split the K loop of an M >= 256 INT4/INT8 product over more workgroups
+ * (fp32 partials, summed in a fixed order: the result does not depend on
+ * the split).  Same role as the rocBLAS workspace behind the reference's
+ * at::mm_out in dequant_matmul_out (hip:1973-1988). */
+R4Q_API int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbits,
+                                     size_t* bytes);
+/* r4q_gemm with a caller-owned workspace of ws_bytes (NULL / 0: no split). */
+R4Q_API int r4q_gemm_ws(const void* x, const void* w, const void* sz, void* y,
+                        int64_t M, int64_t N, int64_t K, int wbits, void* ws,
+                        size_t ws_bytes, void* stream);
 
 /* y[N] = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) (the activation
  * of r4q_res_rmsnorm_fwht / r4q_rmsnorm_fwht, bit-identical) computed inside

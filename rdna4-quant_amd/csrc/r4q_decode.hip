@@ -19,6 +19,7 @@
 // inside the graph, so replaying N tokens needs no host work per token.
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "r4q_ctx.hpp"
@@ -576,13 +577,23 @@ extern "C" int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* 
                           (size_t)(M * D), (size_t)(M * 2 * I), (size_t)(M * I), (size_t)(M * D)};
   size_t total = 0;
   for (size_t sz : sizes) total += align256(sz * 2);
-  R4Q_TRY(ctx->prefill.reserve(total));
+  // split-K partials of the projection GEMMs (the largest any of them uses)
+  size_t gws = 0;
+  for (int li = 0; li < dm.L; ++li) {
+    const r4q_layer& ly = m->layers[li];
+    gws = std::max({gws, gemm_ws_bytes(M, dm.qkvN, D, ly.qkv_bits),
+                    gemm_ws_bytes(M, D, dm.qd, ly.o_bits), gemm_ws_bytes(M, 2 * I, D, ly.gu_bits),
+                    gemm_ws_bytes(M, D, I, ly.down_bits)});
+  }
+  if (logits) gws = std::max(gws, gemm_ws_bytes(M, m->lm_N, m->lm_K, m->lm_bits));
+  R4Q_TRY(ctx->prefill.reserve(total + gws));
   uint16_t* buf[8];
   uint8_t* p = static_cast<uint8_t*>(ctx->prefill.ptr);
   for (int i = 0; i < 8; ++i) {
     buf[i] = reinterpret_cast<uint16_t*>(p);
     p += align256(sizes[i] * 2);
   }
+  void* ws = gws ? p : nullptr;
   uint16_t *x = buf[0], *r = buf[1], *rot = buf[2], *qkv = buf[3], *o = buf[4], *gu = buf[5],
            *y = buf[6], *d = buf[7];
   const float eps = dm.eps;
@@ -594,23 +605,24 @@ extern "C" int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* 
   R4Q_TRY(launch_rownorm(2, x, nullptr, m->layers[0].in_norm, rot, nullptr, M, D, eps, st));
   for (int li = 0; li < dm.L; ++li) {
     const r4q_layer& ly = m->layers[li];
-    R4Q_TRY(gemm_launch(rot, ly.qkv_w, ly.qkv_s, qkv, M, dm.qkvN, D, ly.qkv_bits, st));
+    R4Q_TRY(gemm_launch(rot, ly.qkv_w, ly.qkv_s, qkv, M, dm.qkvN, D, ly.qkv_bits, st, ws, gws));
     R4Q_TRY(launch_head_norm_rope_kv(qkv, dm.qkvN, ly.q_norm, ly.k_norm, qkv, dm.qkvN,
                                      write_kv ? ly.k_cache : nullptr,
                                      write_kv ? ly.v_cache : nullptr, ly.k_scale, ly.v_scale,
                                      m->rope_cos, m->rope_sin, M, dm.H, dm.Hk, eps, dm.max_seq, 0,
                                      nullptr, st, /*prefill_rows=*/true));
     R4Q_TRY(launch_prefill_attention(qkv, dm.qkvN, rot, dm.qd, M, dm.H, dm.Hk, st));
-    R4Q_TRY(gemm_launch(rot, ly.o_w, ly.o_s, o, M, D, dm.qd, ly.o_bits, st));
+    R4Q_TRY(gemm_launch(rot, ly.o_w, ly.o_s, o, M, D, dm.qd, ly.o_bits, st, ws, gws));
     R4Q_TRY(launch_rownorm(3, o, x, ly.post_norm, rot, r, M, D, eps, st));
-    R4Q_TRY(gemm_launch(rot, ly.gu_w, ly.gu_s, gu, M, 2 * I, D, ly.gu_bits, st));
+    R4Q_TRY(gemm_launch(rot, ly.gu_w, ly.gu_s, gu, M, 2 * I, D, ly.gu_bits, st, ws, gws));
     R4Q_TRY(launch_silu(true, gu, gu + I, y, M, I, 2 * I, I, st));
-    R4Q_TRY(gemm_launch(y, ly.down_w, ly.down_s, d, M, D, I, ly.down_bits, st));
+    R4Q_TRY(gemm_launch(y, ly.down_w, ly.down_s, d, M, D, I, ly.down_bits, st, ws, gws));
     const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm
                                       : (m->final_norm ? m->final_norm : m->layers[0].in_norm);
     R4Q_TRY(launch_rownorm(3, d, r, nxt, rot, x, M, D, eps, st));
   }
   if (logits)
-    R4Q_TRY(gemm_launch(rot, m->lm_w, m->lm_s, logits, M, m->lm_N, m->lm_K, m->lm_bits, st));
+    R4Q_TRY(gemm_launch(rot, m->lm_w, m->lm_s, logits, M, m->lm_N, m->lm_K, m->lm_bits, st, ws,
+                        gws));
   return R4Q_OK;
 }

@@ -1,19 +1,24 @@
 // Prefill GEMM Y[M,N] = X[M,K] W[N,K]^T with the weight dequantised on the
-// fly (INT4 / INT8 block-32 asymmetric, or FP16) into LDS and multiplied on
-// the matrix cores with v_mfma_f32_16x16x32_f16 (fp32 accumulate).
+// fly (INT4 / INT8 block-32 asymmetric, or FP16) and multiplied on the
+// matrix cores with v_mfma_f32_16x16x32_f16 (fp32 accumulate).
 //
 // Replaces the reference's prefill projection dequant_matmul_out
 // (hip:1973-1988), which materialises the whole fp16 weight with
 // dequant_int4_kernel and then calls rocBLAS through at::mm_out: here each
 // weight byte is read from HBM once per M-tile and never written back.
 //
-// Tiling: a workgroup (4 waves) owns a 128 x 128 output tile and walks K in
-// steps of 32 (one quantisation block).  Per step the X tile (128 x 32 fp16)
-// and the dequantised W tile (128 x 32 fp16) are staged in LDS (rows padded
-// to 80 B against bank conflicts); each wave computes a 64 x 64 sub-tile as
-// 4 x 4 MFMA 16x16x32 tiles.  The next step's global loads are issued before
-// the current step's MFMAs.  Dequantised values equal r4q_dequant_int4/8
-// bit-for-bit (fp16((q - zp) * scale) from an exact fp32 product).
+// Three kernels, by shape:
+//  * gemm_ring_kernel (M >= 256, INT4 / INT8): 256 x 256 tiles, X and the
+//    raw weights copied global -> LDS through a multi-stage ring, the
+//    weights dequantised once per workgroup into an fp16 B tile, optional
+//    deterministic split-K over a caller workspace (see its comment);
+//  * gemm_mfma_kernel (17 <= M < 256, and FP16 weights): 128 x 128 tiles,
+//    X and the dequantised W staged in LDS per 32-wide K step;
+//  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows.
+// Dequantised values equal r4q_dequant_int4/8 bit-for-bit
+// (fp16((q - zp) * scale) from an exact product, one rounding).
+#include <stdlib.h>
+
 #include "r4q_device.hpp"
 #include "r4q_gemv.hpp"
 #include "r4q_host.hpp"
@@ -106,6 +111,13 @@ __device__ __forceinline__ void store_stage(const Stage<WBITS>& s, uint16_t* As,
   dst[1] = o[1];
 }
 
+// 128 x 128 tile: a workgroup (4 waves) walks K in steps of 32 (one
+// quantisation block).  Per step the X tile (128 x 32 fp16) and the
+// dequantised W tile (128 x 32 fp16) are staged in LDS (rows padded to
+// 80 B); each wave computes a 64 x 64 sub-tile as 4 x 4 MFMA 16x16x32
+// tiles.  The next step's global loads are issued before the current
+// step's MFMAs (one step in flight: latency-bound at large K, which is why
+// M >= 256 takes the ring kernel).
 template <int WBITS>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint16_t* __restrict__ X,
                                                         const uint8_t* __restrict__ W,
@@ -314,6 +326,258 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------
+// Prefill GEMM for M >= 256 with INT4 / INT8 weights: a workgroup of 8 waves
+// (2 per SIMD) owns a 256 x 256 output tile, each wave a 128 x 64 sub-tile
+// (8 x 4 MFMA tiles, 128 fp32 accumulators per lane).
+// The K loop of the 128 x 128 kernel above is bound by global-load latency
+// (one 32-wide K step in flight, ~1.3 us per step on MI355X).  Here X and
+// the raw weight bytes (plus the (scale, zero) words) of a K step land in
+// LDS by direct global->LDS copies (global_load_lds_dwordx4 / _dword) in a
+// ring of Ring::kStages stages, so that several steps are in flight while
+// one is multiplied, without holding them in VGPRs.  The workgroup
+// dequantises the weights of step i+1 (16 elements per thread, natural
+// element order, bit-identical to r4q_dequant_int4/8) into one of two fp16
+// B tiles while step i is multiplied from the other.
+// X rows are 64 bytes per step; the 16-byte piece p of row r sits in LDS
+// slot p ^ ((r >> 1) & 3) of the row, which spreads the fragment reads of
+// consecutive rows over the banks (measured: half the bank conflicts of
+// p ^ ((r >> 2) & 3)).  B tile rows are padded to 80 bytes.
+// One barrier per K step i: before it each wave waits for its own copies of
+// step i+1; after it every wave's copies are visible, the B tile of step i
+// is complete, and every wave is done with step i-1, whose ring slot then
+// receives step i+kStages-1 and whose B tile receives step i+1.  Every wave
+// issues the same number of copies per stage (the wait counts are per
+// wave): the scale words take one copy of waves 0-3, and waves 4-7 repeat
+// theirs into a spare area.
+// Split-K (gridDim.z > 1): split z covers K steps [z*kps, (z+1)*kps) and
+// writes an fp32 partial tile to part[z][M][N], summed in split order by
+// gemm_splitk_reduce_kernel.
+constexpr int RBM = 256, RBN = 256, RBK = 32;
+constexpr int kRingThreads = 512;
+constexpr int kBRow = 40;  // halves per B tile row (32 + 8 pad)
+
+template <int WBITS>
+struct Ring {
+  static constexpr int kStages = WBITS == 4 ? 5 : 4;
+  static constexpr int kX = RBM * RBK * 2;          // X: 16 KB
+  static constexpr int kW = RBN * RBK * WBITS / 8;  // raw weights: 4 KB (INT4) / 8 KB (INT8)
+  static constexpr int kS = RBN * 4;                // (scale, zero) per row
+  static constexpr int kStage = kX + kW + 2 * kS;   // + spare area for waves 4-7
+  static constexpr int kB = RBN * kBRow * 2;        // one fp16 B tile: 20 KB
+  static constexpr int kPerStage = 2 + (WBITS == 4 ? 2 : 1) + 1;  // copies per wave per stage
+};
+
+// Global -> LDS copy of 16 (4) bytes per lane: lane l's bytes land at
+// lds + 16 l (4 l).  Written as inline assembly so that the compiler's
+// wait-count tracking does not see the copies: it would otherwise wait for
+// every copy in flight before any LDS read of the ring; the kernel counts
+// and waits for its own copies (wait_copies) instead.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)((const __attribute__((address_space(3))) void*)p));
+}
+__device__ __forceinline__ void copy16(const void* g, void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr(lds)),
+               "v"(g)
+               : "memory");
+}
+__device__ __forceinline__ void copy4(const void* g, void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_addr(lds)),
+               "v"(g)
+               : "memory");
+}
+
+// Copies K step kb (32 elements) of the workgroup's 256 X rows and 256
+// weight rows into one ring stage; every source row is clamped into the
+// matrix (rows past M / N are computed and not stored).  Wave w copies X
+// rows 32w .. 32w+31 (2 copies of 16 rows x 64 bytes) and weight rows
+// 32w .. 32w+31.
+template <int WBITS>
+__device__ __forceinline__ void ring_issue(uint8_t* stage, const uint16_t* __restrict__ X,
+                                           const uint8_t* __restrict__ W,
+                                           const uint32_t* __restrict__ SZ, int M, int N, int K,
+                                           int m0, int n0, int kb, int wave, int lane) {
+  using R = Ring<WBITS>;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r0 = 32 * wave + 16 * q;  // first row of this copy
+    const int row = r0 + (lane >> 2);
+    const int p = (lane & 3) ^ ((row >> 1) & 3);  // global piece held by LDS slot lane & 3
+    const int m = min(m0 + row, M - 1);
+    copy16(X + (int64_t)m * K + kb * RBK + 8 * p, stage + r0 * 64);
+  }
+  uint8_t* wst = stage + R::kX;
+  if constexpr (WBITS == 4) {  // 16 bytes per row: 2 copies of 16 rows x 4 dwords
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int r0 = 32 * wave + 16 * q;
+      const int64_t n = min(n0 + r0 + (lane >> 2), N - 1);
+      copy4(W + n * (K / 2) + kb * 16 + 4 * (lane & 3), wst + r0 * 16);
+    }
+  } else {  // 32 bytes per row: 32 rows x 2 pieces of 16 bytes
+    const int r0 = 32 * wave;
+    const int64_t n = min(n0 + r0 + (lane >> 1), N - 1);
+    copy16(W + n * K + kb * 32 + 16 * (lane & 1), wst + r0 * 32);
+  }
+  {  // scale words: waves 0-3 rows 64w .. 64w+63; waves 4-7 repeat into the spare area
+    const int r0 = 64 * (wave & 3);
+    const int64_t n = min(n0 + r0 + lane, N - 1);
+    copy4(SZ + n * (K / 32) + kb, stage + R::kX + R::kW + (wave >> 2) * R::kS + r0 * 4);
+  }
+}
+
+// Dequantises half a weight row of one ring stage (16 elements: row t / 2,
+// elements 16 (t % 2) ..) into the fp16 B tile: fp16((q - zp) * scale) as
+// (1024 + q) - (1024 + zp) (exact) times scale (one rounding).
+template <int WBITS>
+__device__ __forceinline__ void ring_dequant(const uint8_t* stage, uint16_t* bt, int t) {
+  using R = Ring<WBITS>;
+  const int row = t >> 1, half = t & 1;
+  const uint32_t s2 = *reinterpret_cast<const uint32_t*>(stage + R::kX + R::kW + row * 4);
+  const uint32_t sb = s2 & 0xFFFFu, zb = s2 >> 16;
+  const h2_t sc = as_h2(sb | (sb << 16));
+  const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
+  uint32_t pr[8];  // (1024 + q_2k, 1024 + q_2k+1) as fp16 pairs
+  if constexpr (WBITS == 4) {
+    const u2_t w = *reinterpret_cast<const u2_t*>(stage + R::kX + row * 16 + 8 * half);
+    typedef uint16_t us2 __attribute__((ext_vector_type(2)));
+    const us2 sh = {0, 4};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t wd = w[k >> 2], b = k & 3;
+      // byte b in both halves, the high half shifted down by 4: (lo nibble, hi nibble)
+      const uint32_t tb = __builtin_amdgcn_perm(0u, wd, (b | 0x0C00u | (b << 16) | 0x0C000000u));
+      const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
+      pr[k] = (nib & 0x000F000Fu) | 0x64006400u;
+    }
+  } else {
+    const u4_t w = *reinterpret_cast<const u4_t*>(stage + R::kX + row * 32 + 16 * half);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t wd = w[k >> 1];
+      pr[k] = __builtin_amdgcn_perm(wd, 0x64646464u, (k & 1) ? 0x00070006u : 0x00050004u);
+    }
+  }
+  u4_t o[2];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k >> 2][k & 3] = as_u32((as_h2(pr[k]) + nz) * sc);
+  u4_t* dst = reinterpret_cast<u4_t*>(bt + row * kBRow + 16 * half);
+  dst[0] = o[0];
+  dst[1] = o[1];
+}
+
+template <int N>
+__device__ __forceinline__ void wait_copies() {  // at most N of this wave's copies outstanding
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier that, unlike __syncthreads, does not first wait for
+// every outstanding global access (the copies still in flight): only for
+// this wave's LDS accesses.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int WBITS>
+__global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, float* __restrict__ part, int M,
+    int N, int K, int kps) {
+  using R = Ring<WBITS>;
+  constexpr int S = R::kStages;
+  __shared__ __align__(16) uint8_t ring[S * R::kStage];
+  __shared__ __align__(16) uint16_t btile[2][RBN * kBRow];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int n0 = blockIdx.x * RBN, m0 = blockIdx.y * RBM;
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+  const int c = lane & 15, g = lane >> 4;
+  const int kb0 = blockIdx.z * kps;
+  const int nk = min(K / RBK - kb0, kps);  // K steps of this split (>= 1)
+
+  f4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  int xoff[8];  // per-lane fragment offsets
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = wm + 16 * i + c;
+    xoff[i] = row * 64 + 16 * (g ^ ((row >> 1) & 3));
+  }
+  const int boff = (wn + c) * kBRow + 8 * g;
+
+  // stages past the split's end repeat its last step (same copy counts in
+  // every iteration; their data is never multiplied)
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    ring_issue<WBITS>(ring + s * R::kStage, X, W, SZ, M, N, K, m0, n0, kb0 + min(s, nk - 1), wave,
+                      lane);
+  wait_copies<(S - 2) * R::kPerStage>();  // step 0
+  ring_barrier();
+  ring_dequant<WBITS>(ring, btile[0], t);
+  for (int i = 0; i < nk; ++i) {
+    wait_copies<(S - 3) * R::kPerStage>();  // this wave's copies of step i+1 landed
+    ring_barrier();
+    ring_issue<WBITS>(ring + ((i + S - 1) % S) * R::kStage, X, W, SZ, M, N, K, m0, n0,
+                      kb0 + min(i + S - 1, nk - 1), wave, lane);
+    const uint8_t* st = ring + (i % S) * R::kStage;
+    const uint16_t* bt = btile[i & 1];
+    h8_t bf[4], af[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const h8_t*>(bt + boff + 16 * j * kBRow);
+#pragma unroll
+    for (int i8 = 0; i8 < 8; ++i8) af[i8] = *reinterpret_cast<const h8_t*>(st + xoff[i8]);
+#pragma unroll
+    for (int i8 = 0; i8 < 8; ++i8)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i8][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i8], bf[j], acc[i8][j], 0, 0, 0);
+    // step i+1's weights dequantised while step i's MFMAs run: LDS reads
+    // first, then one MFMA per two VALU instructions, the B tile writes last
+    ring_dequant<WBITS>(ring + ((i + 1) % S) * R::kStage, btile[(i + 1) & 1], t);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS writes
+  }
+  wait_copies<0>();  // no copy may land after the workgroup's LDS is released
+  // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block
+#pragma unroll
+  for (int i8 = 0; i8 < 8; ++i8)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn + 16 * j + c;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm + 16 * i8 + 4 * g + r;
+        if (row < M && col < N) {
+          if (part)
+            part[((int64_t)blockIdx.z * M + row) * N + col] = acc[i8][j][r];
+          else
+            Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
+        }
+      }
+    }
+}
+
+// Y = fp16(sum over z = 0 .. S-1 of part[z]), in split order (deterministic).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
+                                                                 uint16_t* __restrict__ Y,
+                                                                 int64_t MN, int S) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < MN;
+       i += (int64_t)gridDim.x * 256) {
+    float v = part[i];
+    for (int z = 1; z < S; ++z) v += part[(int64_t)z * MN + i];
+    Y[i] = f2h(v);
+  }
+}
+
 }  // namespace
 
 bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
@@ -345,13 +609,72 @@ int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, in
   return launch_status("gemm_skinny");
 }
 
+bool gemm_ring_ok(int64_t M, int wbits) { return M >= RBM && wbits != 16; }
+
+int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  if (!gemm_ring_ok(M, wbits)) return 1;
+  if (const char* e = getenv("R4Q_GEMM_SPLITS")) {  // tuning override
+    const int64_t v = atoi(e);
+    if (v >= 1 && v <= kMaxGemmSplits && (v == 1 || (size_t)v * M * N * 4 <= ws_bytes) &&
+        K / RBK >= v)
+      return (int)v;
+  }
+  // Estimated time of S splits: the workgroups run in ceil(tiles * S / 256)
+  // rounds of one per CU, each 1/S of a tile's K loop (~3.7 TFLOP/s per
+  // CU measured), plus the fp32 partials written and read back (~5 TB/s).
+  const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
+  const int64_t nk = K / RBK;
+  const double tile_us = 2.0 * RBM * RBN * (double)K / 3.7e6;
+  int best = 1;
+  double best_us = 1e300;
+  for (int S = 1; S <= kMaxGemmSplits; ++S) {
+    if (S > 1 && ((size_t)S * M * N * 4 > ws_bytes || nk / S < 16)) break;
+    const int64_t rounds = (tiles * S + 255) / 256;
+    const double us = (double)rounds * tile_us / S + (S > 1 ? S * (double)M * N * 8 / 5e6 : 0.0);
+    if (us < best_us) {
+      best_us = us;
+      best = S;
+    }
+  }
+  return best;
+}
+
+size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
+  const int S = gemm_splits(M, N, K, wbits, (size_t)-1);
+  return S > 1 ? (size_t)S * M * N * 4 : 0;
+}
+
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
-                     int64_t K, int wbits, hipStream_t st) {
-  const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+                     int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes) {
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
+  if (gemm_ring_ok(M, wbits)) {
+    const int64_t nk = K / RBK;
+    int S = gemm_splits(M, N, K, wbits, ws ? ws_bytes : 0);
+    const int kps = (int)((nk + S - 1) / S);
+    S = (int)((nk + kps - 1) / kps);  // every split non-empty
+    float* part = S > 1 ? static_cast<float*>(ws) : nullptr;
+    const dim3 grid((unsigned)((N + RBN - 1) / RBN), (unsigned)((M + RBM - 1) / RBM),
+                    (unsigned)S);
+    if (wbits == 4)
+      hipLaunchKernelGGL(gemm_ring_kernel<4>, grid, dim3(kRingThreads), 0, st, xp, wp, sp, yp, part,
+                         (int)M, (int)N, (int)K, kps);
+    else
+      hipLaunchKernelGGL(gemm_ring_kernel<8>, grid, dim3(kRingThreads), 0, st, xp, wp, sp, yp, part,
+                         (int)M, (int)N, (int)K, kps);
+    R4Q_TRY(launch_status("gemm_ring"));
+    if (S > 1) {
+      const int64_t MN = M * N;
+      const int64_t blocks = (MN + 255) / 256 < 2048 ? (MN + 255) / 256 : 2048;
+      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                         part, yp, MN, S);
+      R4Q_TRY(launch_status("gemm_splitk_reduce"));
+    }
+    return R4Q_OK;
+  }
+  const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
   switch (wbits) {
     case 4:
       hipLaunchKernelGGL(gemm_mfma_kernel<4>, grid, dim3(256), 0, st, xp, wp, sp, yp, (int)M,

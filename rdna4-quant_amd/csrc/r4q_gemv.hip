@@ -637,8 +637,8 @@ bool gemv_silu_ok(int64_t N, int64_t K, int wbits) {
 }
 
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
-                int64_t K, int wbits, hipStream_t st) {
-  if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st);
+                int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes) {
+  if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes);
   if (gemm_skinny_ok(M, K, wbits)) return gemm_skinny_launch(x, w, sz, y, M, N, K, wbits, st);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* yp = static_cast<uint16_t*>(y);
@@ -659,6 +659,26 @@ extern "C" int r4q_gemm(const void* x, const void* w, const void* sz, void* y, i
   R4Q_REQUIRE(M >= 1, "gemm: M must be >= 1");
   R4Q_TRY(r4q::gemv_check(x, w, sz, y, N, K, wbits));
   return r4q::gemm_launch(x, w, sz, y, M, N, K, wbits, r4q::as_stream(stream));
+}
+
+extern "C" int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbits,
+                                        size_t* bytes) {
+  R4Q_REQUIRE(bytes, "gemm_workspace_bytes: null output");
+  R4Q_REQUIRE(M >= 1 && N >= 1 && K >= 32 && K % 32 == 0 &&
+                  (wbits == 4 || wbits == 8 || wbits == 16),
+              "gemm_workspace_bytes: bad shape or format");
+  *bytes = M > r4q::kSkinnyMaxRows ? r4q::gemm_ws_bytes(M, N, K, wbits) : 0;
+  return R4Q_OK;
+}
+
+extern "C" int r4q_gemm_ws(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                           int64_t N, int64_t K, int wbits, void* ws, size_t ws_bytes,
+                           void* stream) {
+  R4Q_REQUIRE(M >= 1, "gemm: M must be >= 1");
+  R4Q_TRY(r4q::gemv_check(x, w, sz, y, N, K, wbits));
+  R4Q_REQUIRE(ws || ws_bytes == 0, "gemm: workspace size without a workspace");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "gemm: workspace must be 16-byte aligned");
+  return r4q::gemm_launch(x, w, sz, y, M, N, K, wbits, r4q::as_stream(stream), ws, ws_bytes);
 }
 
 extern "C" int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const void* gamma,

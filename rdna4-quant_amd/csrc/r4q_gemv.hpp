@@ -28,9 +28,17 @@ bool gemv_silu_ok(int64_t N, int64_t K, int wbits);
 // MFMA tile GEMM with on-the-fly dequantisation.
 constexpr int64_t kSkinnyMaxRows = 16;
 
-// MFMA GEMM (r4q_gemm.hip), arguments validated by the caller.
+// MFMA GEMM (r4q_gemm.hip), arguments validated by the caller.  ws
+// (ws_bytes of device memory, may be null) holds the fp32 partials of a
+// split-K launch; gemm_splits() gives the split count a workspace allows
+// (1: none needed).
+constexpr int kMaxGemmSplits = 8;
+int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes);
+// Workspace bytes for the best split count of a shape (0: none needed).
+size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits);
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
-                     int64_t K, int wbits, hipStream_t st);
+                     int64_t K, int wbits, hipStream_t st, void* ws = nullptr,
+                     size_t ws_bytes = 0);
 
 // Skinny MFMA GEMM for 2 <= M <= 16 rows (weights streamed once); usable
 // when gemm_skinny_ok(M, K, wbits).
@@ -38,8 +46,9 @@ bool gemm_skinny_ok(int64_t M, int64_t K, int wbits);
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                        int64_t N, int64_t K, int wbits, hipStream_t st);
 
-// y[M,N] = x[M,K] W^T; rows of x and y contiguous.
+// y[M,N] = x[M,K] W^T; rows of x and y contiguous.  ws: optional split-K
+// workspace (see gemm_mfma_launch).
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
-                int64_t K, int wbits, hipStream_t st);
+                int64_t K, int wbits, hipStream_t st, void* ws = nullptr, size_t ws_bytes = 0);
 
 }  // namespace r4q

@@ -123,8 +123,12 @@ def dbg_gemm(X: torch.Tensor, W: torch.Tensor, S: torch.Tensor, M: int, N: int,
     _need(X.numel() == M * K, "X size != M*K")
     bits = weight_bits(W, K)
     Y = torch.empty((M, N), dtype=torch.float16, device=X.device)
-    _R.call("r4q_gemm", X.data_ptr(), W.data_ptr(), None if bits == 16 else S.data_ptr(),
-            Y.data_ptr(), M, N, K, bits, _stream())
+    nws = C.c_size_t(0)
+    _R.call("r4q_gemm_workspace_bytes", M, N, K, bits, C.byref(nws))
+    ws = torch.empty(nws.value, dtype=torch.uint8, device=X.device) if nws.value else None
+    _R.call("r4q_gemm_ws", X.data_ptr(), W.data_ptr(), None if bits == 16 else S.data_ptr(),
+            Y.data_ptr(), M, N, K, bits, None if ws is None else ws.data_ptr(), nws.value,
+            _stream())
     return Y
 
 

@@ -68,6 +68,64 @@ def test_skinny_gemm_one_hot_columns_exact(dev, bits):
         assert np.array_equal(y[r], W[:, k]), k
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (257, 520, 32), (600, 256, 4096),
+                                   (512, 7168, 5120), (256, 255, 96)])
+def test_ring_gemm_ragged_and_split(dev, bits, M, N, K):
+    """M >= 256: the 256 x 256 LDS-ring kernel, with ragged M / N tiles,
+    K loops shorter than the copy ring (K = 32, 96), and split-K over a
+    workspace (few tiles, long K)."""
+    got, want = _run(dev, bits, M, N, K, seed=M + 3 * N + K + bits)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= TOL
+    for r in (0, M // 2, M - 1):
+        assert rel_l2(got[r], want[r]) <= TOL, r
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("N,K", [(700, 1024), (300, 8192)])
+def test_ring_gemm_one_hot_columns_exact(dev, bits, N, K):
+    """Row r of x = e_k(r) over 300 rows: y[r] is column k(r) of the
+    dequantised weight, bit for bit -- in one pass and with the K loop split
+    (fp32 partials of zeros and one exact product)."""
+    g = S.gen(43 + bits + K)
+    M = 300
+    w, sz = S.weight(N, K, bits, g)
+    W = O.dequant(w.numpy(), sz.numpy(), bits)
+    ks = [(r * 997 + r // 7) % K for r in range(M)]
+    x = torch.zeros(M, K, dtype=torch.float16)
+    for r, k in enumerate(ks):
+        x[r, k] = 1.0
+    y = int4_hip.dbg_gemm(x.to(dev), w.to(dev), sz.to(dev), M, N, K).cpu().numpy()
+    for r, k in enumerate(ks):
+        assert np.array_equal(y[r], W[:, k]), (r, k)
+
+
+def test_ring_gemm_split_matches_unsplit(dev):
+    """The split-K result equals the one-pass result within fp32 rounding."""
+    import ctypes as C
+    import r4q_lib as R
+    g = S.gen(77)
+    M, N, K = 512, 768, 8192
+    w, sz = S.int4_weight(N, K, g)
+    x = torch.randn(M, K, generator=g).half()
+    X, Wd, SZ = x.to(dev), w.to(dev), sz.to(dev)
+    nws = C.c_size_t(0)
+    R.call("r4q_gemm_workspace_bytes", M, N, K, 4, C.byref(nws))
+    assert nws.value > 0  # this shape splits
+    ws = torch.empty(nws.value, dtype=torch.uint8, device=dev)
+    y1 = torch.empty(M, N, dtype=torch.float16, device=dev)
+    y2 = torch.empty(M, N, dtype=torch.float16, device=dev)
+    R.call("r4q_gemm", X.data_ptr(), Wd.data_ptr(), SZ.data_ptr(), y1.data_ptr(), M, N, K, 4,
+           R.stream_handle())
+    R.call("r4q_gemm_ws", X.data_ptr(), Wd.data_ptr(), SZ.data_ptr(), y2.data_ptr(), M, N, K, 4,
+           ws.data_ptr(), nws.value, R.stream_handle())
+    a, b = y1.float().cpu().numpy(), y2.float().cpu().numpy()
+    assert rel_l2(b, a) <= 1e-3
+    want = O.gemm(x.numpy(), w.numpy(), sz.numpy(), 4)
+    assert rel_l2(b, want) <= TOL
+
+
 def test_small_m_path_matches_gemv(dev):
     """M <= 16 rows agree with the batch-1 GEMV row by row (different
     accumulation order: tolerance, not bits)."""
