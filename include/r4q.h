@@ -47,6 +47,7 @@
  *                           and decode_loop (:3284-3466) via tokens_out
  *   r4q_decode_profile   <- decode_profile          (:3047-3273)
  *   r4q_prefill_logits   <- prefill_logits          (:2127-2320)
+ *   r4q_prefill_attention <- its causal SDPA + FWHT-32 (:2254-2269)
  *   r4q_decode_generate, r4q_sample <- the Python sampling of the engine
  *                           (int4_engine_v5.py:330-335, 387-399)
  */
@@ -291,6 +292,15 @@ R4Q_API int r4q_hbm_read(const void* src, int64_t bytes, void* sink, int64_t sin
  * write_kv != 0, the FP8 KV caches at positions 0..M-1. */
 R4Q_API int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* ids,
                        int64_t M, void* logits, int write_kv, void* stream);
+/* The prefill's causal GQA self-attention alone (the step r4q_prefill_logits
+ * runs after the head norm + RoPE): qkv rows [M, stride] fp16 hold H query
+ * heads, then Hk key and Hk value heads of head_dim 128; out[M, out_stride]
+ * gets FWHT32(softmax_{j<=m}(q_m . k_j / sqrt(128)) V) per query head.
+ * Replaces the causal SDPA of int4_prefill_logits (hip:2254-2265) and the
+ * FWHT-32 after it (hip:2269). */
+R4Q_API int r4q_prefill_attention(const void* qkv, int64_t stride, void* out,
+                                  int64_t out_stride, int64_t M, int64_t H, int64_t Hk,
+                                  void* stream);
 
 #ifdef __cplusplus
 }

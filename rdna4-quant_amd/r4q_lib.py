@@ -66,6 +66,7 @@ SIGNATURES = {
     "r4q_fp8_to_fp16": [_p, _p, _i64, _p],
     "r4q_gemv": [_p, _p, _p, _p, _i64, _i64, C.c_int, _p],
     "r4q_gemm": [_p, _p, _p, _p, _i64, _i64, _i64, C.c_int, _p],
+    "r4q_prefill_attention": [_p, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_gemm_workspace_bytes": [_i64, _i64, _i64, C.c_int, C.POINTER(C.c_size_t)],
     "r4q_gemm_ws": [_p, _p, _p, _p, _i64, _i64, _i64, C.c_int, _p, C.c_size_t, _p],
     "r4q_rmsnorm": [_p, _p, _p, _i64, _i64, _f32, _p],

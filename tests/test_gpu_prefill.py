@@ -109,3 +109,28 @@ def test_prefill_rejects_bad_token_and_length(dev):
         gpu_prefill(m, np.array([1, 2, 100]))
     with pytest.raises(RuntimeError):
         gpu_prefill(m, np.arange(17) % 100, write_kv=True)  # beyond the cache
+
+
+@pytest.mark.parametrize("H,Hk", [(40, 8), (4, 4), (8, 2)])
+@pytest.mark.parametrize("M", [1, 17, 64, 65, 200, 512])
+def test_prefill_attention_vs_oracle(dev, M, H, Hk):
+    """The prompt's causal GQA attention (r4q_prefill_attention) alone:
+    ragged query blocks (M not a multiple of 64 or of the 32-key block),
+    single-row prompts and group sizes 1, 4, 5, against float64 SDPA with
+    the FWHT-32 rotation."""
+    import r4q_lib as R
+    g = torch.Generator().manual_seed(1000 + M + H)
+    stride = (H + 2 * Hk) * 128 + 64  # padded rows
+    qkv = (torch.randn(M, stride, generator=g) * 1.5).half()
+    q = qkv[:, :H * 128].reshape(M, H, 128)
+    k = qkv[:, H * 128:(H + Hk) * 128].reshape(M, Hk, 128)
+    v = qkv[:, (H + Hk) * 128:(H + 2 * Hk) * 128].reshape(M, Hk, 128)
+    want = O.attention_prefill(q.numpy(), k.numpy(), v.numpy(), H, Hk, fwht=True)
+    out = torch.empty(M, H * 128 + 32, dtype=torch.float16, device=dev)
+    R.call("r4q_prefill_attention", qkv.to(dev).data_ptr(), stride, out.data_ptr(), H * 128 + 32,
+           M, H, Hk, R.stream_handle())
+    got = out[:, :H * 128].cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= TOL
+    for r in sorted({0, M // 2, M - 1}):
+        assert rel_l2(got[r], want[r]) <= TOL, r
