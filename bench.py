@@ -34,6 +34,7 @@ sys.path.insert(0, PKG)
 
 METRIC = "INT4 GEMV HBM GB/s (% of peak); decode tok/s at ctx=2048, batch 1"
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16
 ROOFLINE_KERNEL = "gemv_kernel<4, 32, 5, 1, false, false>"
 # Counter-derived HBM bytes per launch of ROOFLINE_KERNEL (FETCH_SIZE + WRITE_SIZE
 # passes, calibrated against a copy of known size), written by that measurement.
@@ -203,6 +204,52 @@ def read_floor(dev, iters=200, copies=8):
     return e0.elapsed_time(e1) * 1000.0 / (reps * iters), nbytes
 
 
+def prefill_gemm_leg(dev, iters=20):
+    """Config 3: Y[512, N] = X[512, K] deq(W)^T with INT4 weights (config 0's
+    distribution), (K, N) = (5120, 17408) and (17408, 5120), through
+    r4q_gemm_ws with the split-K workspace the library asks for.  HIP events
+    on a private stream; returns {shape: {us, tflops, frac, splits}}."""
+    import ctypes as C
+
+    import torch
+
+    import r4q_lib as R
+    import r4q_synth as S
+    res = {}
+    st = torch.cuda.Stream(dev)
+    for K, N in ((5120, 17408), (17408, 5120)):
+        M = 512
+        g = S.gen(3)
+        w, sz = S.int4_weight(N, K, g)
+        x = torch.randn(M, K, generator=g).half()
+        X, Wd, SZ = x.to(dev), w.to(dev), sz.to(dev)
+        Y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        nws = C.c_size_t(0)
+        R.call("r4q_gemm_workspace_bytes", M, N, K, 4, C.byref(nws))
+        ws = torch.empty(max(nws.value, 16), dtype=torch.uint8, device=dev)
+
+        def launch():
+            R.call("r4q_gemm_ws", X.data_ptr(), Wd.data_ptr(), SZ.data_ptr(), Y.data_ptr(), M, N,
+                   K, 4, ws.data_ptr(), nws.value, st.cuda_stream)
+
+        for _ in range(5):
+            launch()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(iters):
+            launch()
+        e1.record(st)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        tflops = 2.0 * M * N * K / us / 1e6
+        res[f"{K}x{N}"] = {"us": round(us, 2), "tflops": round(tflops, 1),
+                           "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4),
+                           "splits": nws.value // (M * N * 4) if nws.value else 1}
+        del X, Wd, SZ, Y, ws
+    return res
+
+
 def flash_decode_leg(dev, ctx, iters=100):
     """Config 2: r4q_flash_decode at batch 1, 40 query / 8 KV heads, cold KV.
 
@@ -325,6 +372,9 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the config-3 prefill GEMM leg (the program the MFMA "
+                         "counter runs profile)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline GEMV loop and the copy calibration "
                          "(the program the counter runs profile)")
@@ -338,6 +388,9 @@ def main():
 
     import int4_hip
     dev = torch.device("cuda:0")
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": prefill_gemm_leg(dev)}), flush=True)
+        return
     if args.roofline_only:
         us, alg = gemv_roofline(dev, eager_tail=2 * 8)
         rf_us, rf_bytes = read_floor(dev)
@@ -360,6 +413,11 @@ def main():
                         "gbps": round(a_bytes / a_us / 1e3, 1),
                         "frac": round(a_bytes / a_us / 1e3 / HBM_PEAK_GBPS, 4)}
         log(f"flash-decode ctx={c}: {a_us:.2f} us, {a_bytes / a_us / 1e3:.0f} GB/s (cold KV)")
+    torch.cuda.empty_cache()
+    pgemm = prefill_gemm_leg(dev)
+    for k, v in pgemm.items():
+        log(f"prefill GEMM 512x{k.replace('x', ' -> ')} INT4: {v['us']:.1f} us, "
+            f"{v['tflops']:.0f} TFLOP/s ({v['frac'] * 100:.1f}% of fp16 MFMA peak)")
     torch.cuda.empty_cache()
 
     log("building synthetic model")
@@ -458,6 +516,8 @@ def main():
         },
         # config 2: flash-decode alone, batch 1, cold KV (ring > 512 MB), per ctx
         "flash_decode": attn,
+        # config 3: prefill GEMM, M = 512, INT4, K x N, fraction of 2.5 PF fp16 MFMA
+        "prefill_gemm": pgemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -350,9 +350,14 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 // issues the same number of copies per stage (the wait counts are per
 // wave): the scale words take one copy of waves 0-3, and waves 4-7 repeat
 // theirs into a spare area.
-// Split-K (gridDim.z > 1): split z covers K steps [z*kps, (z+1)*kps) and
-// writes an fp32 partial tile to part[z][M][N], summed in split order by
-// gemm_splitk_reduce_kernel.
+// Work split (1-D grid, tiles numbered M-tile-major): blocks 0 .. full-1
+// each compute a whole tile and write fp16; the remaining nst tiles are
+// split S ways along K -- block full + S j + s covers K steps
+// [s*kps, (s+1)*kps) of tile full + j and writes its fp32 partial to
+// part[s][j] (256 x 256) -- and gemm_splitk_reduce_kernel sums the S
+// partials of each split tile in split order (deterministic).  With
+// full = 0 every tile is split; with full a multiple of the CU count only
+// the last round's tiles are, so that round keeps every CU busy.
 constexpr int RBM = 256, RBN = 256, RBK = 32;
 constexpr int kRingThreads = 512;
 constexpr int kBRow = 40;  // halves per B tile row (32 + 8 pad)
@@ -483,17 +488,22 @@ template <int WBITS>
 __global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
     const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, float* __restrict__ part, int M,
-    int N, int K, int kps) {
+    int N, int K, int full, int nsplit, int kps) {
   using R = Ring<WBITS>;
   constexpr int S = R::kStages;
   __shared__ __align__(16) uint8_t ring[S * R::kStage];
   __shared__ __align__(16) uint16_t btile[2][RBN * kBRow];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int n0 = blockIdx.x * RBN, m0 = blockIdx.y * RBM;
+  const int b = blockIdx.x;
+  const bool split = b >= full;  // workgroup-uniform
+  const int slot = split ? (b - full) / nsplit : 0, sp = split ? (b - full) % nsplit : 0;
+  const int tile = split ? full + slot : b, ntn = (N + RBN - 1) / RBN;
+  const int n0 = (tile % ntn) * RBN, m0 = (tile / ntn) * RBM;
   const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
   const int c = lane & 15, g = lane >> 4;
-  const int kb0 = blockIdx.z * kps;
-  const int nk = min(K / RBK - kb0, kps);  // K steps of this split (>= 1)
+  const int kb0 = split ? sp * kps : 0;
+  const int nk = split ? min(K / RBK - kb0, kps) : K / RBK;  // K steps of this block (>= 1)
+  const int nst = (int)(gridDim.x - full) / nsplit;  // split tiles
 
   f4_t acc[8][4];
 #pragma unroll
@@ -556,26 +566,30 @@ __global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + wm + 16 * i8 + 4 * g + r;
-        if (row < M && col < N) {
-          if (part)
-            part[((int64_t)blockIdx.z * M + row) * N + col] = acc[i8][j][r];
-          else
-            Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
-        }
+        if (split)  // the whole 256 x 256 partial tile (the reduction skips the outside)
+          part[(((int64_t)sp * nst + slot) * RBM + (row - m0)) * RBN + (col - n0)] = acc[i8][j][r];
+        else if (row < M && col < N)
+          Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
       }
     }
 }
 
-// Y = fp16(sum over z = 0 .. S-1 of part[z]), in split order (deterministic).
+// Y = fp16(sum over s = 0 .. S-1 of part[s][slot]) for the nst split tiles
+// (tiles full .. full+nst-1), in split order (deterministic); one block per
+// (split tile, tile row), one thread per column.
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
-                                                                 uint16_t* __restrict__ Y,
-                                                                 int64_t MN, int S) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < MN;
-       i += (int64_t)gridDim.x * 256) {
-    float v = part[i];
-    for (int z = 1; z < S; ++z) v += part[(int64_t)z * MN + i];
-    Y[i] = f2h(v);
-  }
+                                                                 uint16_t* __restrict__ Y, int M,
+                                                                 int N, int full, int nst,
+                                                                 int S) {
+  const int slot = blockIdx.x / RBM, r = blockIdx.x % RBM, c = threadIdx.x;
+  const int tile = full + slot, ntn = (N + RBN - 1) / RBN;
+  const int row = (tile / ntn) * RBM + r, col = (tile % ntn) * RBN + c;
+  if (row >= M || col >= N) return;
+  const int64_t plane = (int64_t)nst * RBM * RBN;
+  const float* p = part + ((int64_t)slot * RBM + r) * RBN + c;
+  float v = p[0];
+  for (int z = 1; z < S; ++z) v += p[z * plane];
+  Y[(int64_t)row * N + col] = f2h(v);
 }
 
 }  // namespace
@@ -611,37 +625,77 @@ int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, in
 
 bool gemm_ring_ok(int64_t M, int wbits) { return M >= RBM && wbits != 16; }
 
-int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
-  if (!gemm_ring_ok(M, wbits)) return 1;
-  if (const char* e = getenv("R4Q_GEMM_SPLITS")) {  // tuning override
-    const int64_t v = atoi(e);
-    if (v >= 1 && v <= kMaxGemmSplits && (v == 1 || (size_t)v * M * N * 4 <= ws_bytes) &&
-        K / RBK >= v)
-      return (int)v;
-  }
-  // Estimated time of S splits: the workgroups run in ceil(tiles * S / 256)
-  // rounds of one per CU, each 1/S of a tile's K loop (~3.7 TFLOP/s per
-  // CU measured), plus the fp32 partials written and read back (~5 TB/s).
+// Work split of the ring kernel: `full` tiles computed whole, the other
+// nst = tiles - full split S ways along K (kps steps each).
+struct RingPlan {
+  int full = 0, S = 1, kps = 0, nst = 0;
+  size_t ws = 0;  // fp32 partials: S * nst * 256 * 256 * 4 bytes
+};
+
+RingPlan ring_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
+  // Estimated time: rounds of one workgroup per CU (256), a whole tile's K
+  // loop at ~3.7 TFLOP/s per CU (measured), split tiles taking 1/S of it,
+  // plus the partials written and read back at ~5 TB/s.  Candidates: no
+  // split; every tile split S ways (few tiles); only the tiles of a last,
+  // partial round split S ways (full = the tiles of the complete rounds).
   const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
   const int64_t nk = K / RBK;
   const double tile_us = 2.0 * RBM * RBN * (double)K / 3.7e6;
-  int best = 1;
-  double best_us = 1e300;
-  for (int S = 1; S <= kMaxGemmSplits; ++S) {
-    if (S > 1 && ((size_t)S * M * N * 4 > ws_bytes || nk / S < 16)) break;
-    const int64_t rounds = (tiles * S + 255) / 256;
-    const double us = (double)rounds * tile_us / S + (S > 1 ? S * (double)M * N * 8 / 5e6 : 0.0);
+  const double part_us = (double)RBM * RBN * 8 / 5e6;  // one partial tile, out and back
+  RingPlan best;
+  best.full = (int)tiles;
+  best.kps = (int)nk;
+  double best_us = (double)((tiles + 255) / 256) * tile_us;
+  auto consider = [&](int64_t full, int S) {
+    const int64_t nst = tiles - full;
+    if (S < 2 || nst <= 0 || nk / S < 8) return;
+    const size_t ws = (size_t)S * nst * RBM * RBN * 4;
+    if (ws > ws_bytes) return;
+    const int64_t rounds_full = (full + 255) / 256, rounds_split = (nst * S + 255) / 256;
+    const double us = rounds_full * tile_us + rounds_split * tile_us / S + S * nst * part_us;
     if (us < best_us) {
       best_us = us;
-      best = S;
+      best.full = (int)full;
+      best.S = S;
+      best.nst = (int)nst;
+      best.ws = ws;
     }
+  };
+  for (int S = 2; S <= kMaxGemmSplits; ++S) {
+    consider(0, S);
+    if (tiles > 256 && tiles % 256) consider(tiles - tiles % 256, S);
+  }
+  if (const char* e = getenv("R4Q_GEMM_SPLITS")) {  // tuning override: every tile split
+    const int v = atoi(e);
+    const size_t ws = (size_t)v * tiles * RBM * RBN * 4;
+    if (v >= 2 && v <= kMaxGemmSplits && nk / v >= 1 && ws <= ws_bytes) {
+      best.full = 0;
+      best.S = v;
+      best.nst = (int)tiles;
+      best.ws = ws;
+    } else if (v == 1) {
+      best = RingPlan();
+      best.full = (int)tiles;
+    }
+  }
+  best.kps = best.S > 1 ? (int)((nk + best.S - 1) / best.S) : (int)nk;
+  if (best.S > 1) best.S = (int)((nk + best.kps - 1) / best.kps);  // every split non-empty
+  if (best.S == 1) {
+    best.full = (int)tiles;
+    best.nst = 0;
+    best.ws = 0;
+  } else {
+    best.ws = (size_t)best.S * best.nst * RBM * RBN * 4;
   }
   return best;
 }
 
+int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  return gemm_ring_ok(M, wbits) ? ring_plan(M, N, K, ws_bytes).S : 1;
+}
+
 size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
-  const int S = gemm_splits(M, N, K, wbits, (size_t)-1);
-  return S > 1 ? (size_t)S * M * N * 4 : 0;
+  return gemm_ring_ok(M, wbits) ? ring_plan(M, N, K, (size_t)-1).ws : 0;
 }
 
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
@@ -651,25 +705,19 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
   if (gemm_ring_ok(M, wbits)) {
-    const int64_t nk = K / RBK;
-    int S = gemm_splits(M, N, K, wbits, ws ? ws_bytes : 0);
-    const int kps = (int)((nk + S - 1) / S);
-    S = (int)((nk + kps - 1) / kps);  // every split non-empty
-    float* part = S > 1 ? static_cast<float*>(ws) : nullptr;
-    const dim3 grid((unsigned)((N + RBN - 1) / RBN), (unsigned)((M + RBM - 1) / RBM),
-                    (unsigned)S);
+    const RingPlan pl = ring_plan(M, N, K, ws ? ws_bytes : 0);
+    float* part = pl.S > 1 ? static_cast<float*>(ws) : nullptr;
+    const unsigned blocks = (unsigned)(pl.full + (int64_t)pl.nst * pl.S);
     if (wbits == 4)
-      hipLaunchKernelGGL(gemm_ring_kernel<4>, grid, dim3(kRingThreads), 0, st, xp, wp, sp, yp, part,
-                         (int)M, (int)N, (int)K, kps);
+      hipLaunchKernelGGL(gemm_ring_kernel<4>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
+                         yp, part, (int)M, (int)N, (int)K, pl.full, pl.S, pl.kps);
     else
-      hipLaunchKernelGGL(gemm_ring_kernel<8>, grid, dim3(kRingThreads), 0, st, xp, wp, sp, yp, part,
-                         (int)M, (int)N, (int)K, kps);
+      hipLaunchKernelGGL(gemm_ring_kernel<8>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
+                         yp, part, (int)M, (int)N, (int)K, pl.full, pl.S, pl.kps);
     R4Q_TRY(launch_status("gemm_ring"));
-    if (S > 1) {
-      const int64_t MN = M * N;
-      const int64_t blocks = (MN + 255) / 256 < 2048 ? (MN + 255) / 256 : 2048;
-      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                         part, yp, MN, S);
+    if (pl.S > 1) {
+      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)(pl.nst * RBM)), dim3(256), 0,
+                         st, part, yp, (int)M, (int)N, pl.full, pl.nst, pl.S);
       R4Q_TRY(launch_status("gemm_splitk_reduce"));
     }
     return R4Q_OK;

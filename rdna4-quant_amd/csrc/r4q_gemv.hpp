@@ -32,7 +32,7 @@ constexpr int64_t kSkinnyMaxRows = 16;
 // (ws_bytes of device memory, may be null) holds the fp32 partials of a
 // split-K launch; gemm_splits() gives the split count a workspace allows
 // (1: none needed).
-constexpr int kMaxGemmSplits = 8;
+constexpr int kMaxGemmSplits = 16;
 int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes);
 // Workspace bytes for the best split count of a shape (0: none needed).
 size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits);
