@@ -257,7 +257,7 @@ __device__ __forceinline__ h8_t skinny_a(const uint16_t* __restrict__ xrow, int 
   }
 }
 
-template <int WBITS, int T>
+template <int WBITS, int T, int U, bool ROLL>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint32_t* __restrict__ SZ,
@@ -267,7 +267,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   constexpr int NM = Skinny<WBITS>::kMfma;
   constexpr int CK = KPI / 4;  // elements per lane chunk
   __shared__ __align__(16) float red[4][T][64][4];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // The wave index is made a scalar so that the K loop and the per-batch
+  // guards below are scalar branches: an MFMA computes its whole tile
+  // whatever EXEC holds, so a guard lowered to an EXEC mask would not skip it.
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int g = lane >> 4, r16 = lane & 15;
   const int n0 = blockIdx.x * 16 * T;
   const int iters = K / KPI;
@@ -279,13 +282,17 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 #pragma unroll
   for (int i = 0; i < T; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // U iterations per batch: all their loads are issued before any MFMA
-  // (iterations past the end load the last one again and are not computed)
-  constexpr int U = 4;
-  for (int it0 = wave; it0 < iters; it0 += 4 * U) {
+  // Batches of U iterations (iterations past the end load the last one
+  // again and are not computed).  ROLL: two register sets, the next batch's
+  // loads issued before the current batch is multiplied, so a batch is
+  // always in flight -- faster when the grid has few workgroups (N <= 7168:
+  // 10-20%), slower when it has many (gate_up: 57 -> 62 us at batch 8).
+  struct Batch {
     u4_t wv[U][T];
     uint32_t s2[U][T];
     h8_t a[U][NM];
+  };
+  auto load = [&](Batch& bt, int it0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int it = min(it0 + 4 * u, iters - 1);
@@ -293,13 +300,15 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         const int64_t n = min(n0 + 16 * i + r16, N - 1);  // clamped: in bounds
-        wv[u][i] = __builtin_nontemporal_load(
+        bt.wv[u][i] = __builtin_nontemporal_load(
             reinterpret_cast<const u4_t*>(W + n * row_bytes + (int64_t)kchunk * WBITS / 8));
-        s2[u][i] = (WBITS == 16) ? 0u : SZ[n * nb + kchunk / 32];
+        bt.s2[u][i] = (WBITS == 16) ? 0u : SZ[n * nb + kchunk / 32];
       }
 #pragma unroll
-      for (int d = 0; d < NM; ++d) a[u][d] = skinny_a<WBITS>(xrow, kchunk, d);
+      for (int d = 0; d < NM; ++d) bt.a[u][d] = skinny_a<WBITS>(xrow, kchunk, d);
     }
+  };
+  auto compute = [&](const Batch& bt, int it0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (it0 + 4 * u < iters) {  // wave-uniform
@@ -308,8 +317,24 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 #pragma unroll
           for (int d = 0; d < NM; ++d)
             acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                a[u][d], skinny_b<WBITS>(wv[u][i], s2[u][i], d), acc[i], 0, 0, 0);
+                bt.a[u][d], skinny_b<WBITS>(bt.wv[u][i], bt.s2[u][i], d), acc[i], 0, 0, 0);
       }
+    }
+  };
+  if constexpr (ROLL) {
+    Batch b0, b1;
+    load(b0, wave);
+    for (int it0 = wave; it0 < iters; it0 += 8 * U) {
+      load(b1, it0 + 4 * U);
+      compute(b0, it0);
+      load(b0, it0 + 8 * U);
+      compute(b1, it0 + 4 * U);
+    }
+  } else {
+    for (int it0 = wave; it0 < iters; it0 += 4 * U) {
+      Batch b0;
+      load(b0, it0);
+      compute(b0, it0);
     }
   }
 #pragma unroll
@@ -602,24 +627,33 @@ bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                        int64_t N, int64_t K, int wbits, hipStream_t st) {
   constexpr int T = 2;
-  const dim3 grid((unsigned)((N + 16 * T - 1) / (16 * T)));
+  const int64_t wgs = (N + 16 * T - 1) / (16 * T);
+  const dim3 grid((unsigned)wgs);
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
+  // rolling two-set batches of 2 for small grids, single batches of 4 for
+  // grids that fill the chip several times over (measured at batch 8)
+  const bool roll = wgs < 512;
+#define R4Q_SKINNY(WB)                                                                        \
+  if (roll)                                                                                   \
+    hipLaunchKernelGGL((gemm_skinny_kernel<WB, T, 2, true>), grid, dim3(256), 0, st, xp, wp,   \
+                       sp, yp, (int)M, (int)N, (int)K);                                       \
+  else                                                                                        \
+    hipLaunchKernelGGL((gemm_skinny_kernel<WB, T, 4, false>), grid, dim3(256), 0, st, xp, wp,  \
+                       sp, yp, (int)M, (int)N, (int)K);
   switch (wbits) {
     case 4:
-      hipLaunchKernelGGL((gemm_skinny_kernel<4, T>), grid, dim3(256), 0, st, xp, wp, sp, yp,
-                         (int)M, (int)N, (int)K);
+      R4Q_SKINNY(4)
       break;
     case 8:
-      hipLaunchKernelGGL((gemm_skinny_kernel<8, T>), grid, dim3(256), 0, st, xp, wp, sp, yp,
-                         (int)M, (int)N, (int)K);
+      R4Q_SKINNY(8)
       break;
     default:
-      hipLaunchKernelGGL((gemm_skinny_kernel<16, T>), grid, dim3(256), 0, st, xp, wp, sp, yp,
-                         (int)M, (int)N, (int)K);
+      R4Q_SKINNY(16)
   }
+#undef R4Q_SKINNY
   return launch_status("gemm_skinny");
 }
 
