@@ -139,6 +139,21 @@ R4Q_API int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* gamm
                           void* res_out, float eps, const void* w, const void* sz,
                           void* y, int64_t I, int64_t K, int wbits, void* stream);
 
+/* The same pair split at the FWHT, as the decode step runs it: r4q_gate_up_silu
+ * writes h[I] = silu(fp16(g)) * fp16(u) as fp32 (arguments as
+ * r4q_gate_up_silu_fwht, h 4-byte aligned), and r4q_fwht_gemv computes
+ * y = W x with x = fp16(FWHT32(h)) per 32 elements (K % 32 == 0), x
+ * bit-identical to r4q_silu_mul_fwht's output, so y equals r4q_gemv of that
+ * output.  Gate and up rows of the same index are reduced by the same lanes,
+ * so no workgroup has to own 64-row units and the grid size is free.
+ * Replace the launch_gemv (gate_up) -> silu_hadamard_ds -> launch_gemv (down)
+ * chain of the reference's decode step (hip:2508-2516). */
+R4Q_API int r4q_gate_up_silu(const void* a, const void* b, const void* gamma, void* res_out,
+                     float eps, const void* w, const void* sz, float* h, int64_t I,
+                     int64_t K, int wbits, void* stream);
+R4Q_API int r4q_fwht_gemv(const float* h, const void* w, const void* sz, void* y, int64_t N,
+                  int64_t K, int wbits, void* stream);
+
 /* ------------------------------------------------------ norms / rotations */
 
 /* y = fp16(x * rrms * w), rrms = 1/sqrt(mean(x^2) + eps), per row of D. */

@@ -196,11 +196,18 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
     // gate/up: r = fp16(o + h), RMSNorm + FWHT in the staging and, for
-    // INT4/INT8, the SiLU-gate + FWHT in the epilogue (y written directly)
+    // INT4/INT8, silu(g) * u in the epilogue as fp32 (in bf.gu, unused at
+    // batch 1); the down GEMV applies the FWHT-32 in its staging
     const bool silu_fused = fused && y.gu_bits != 16 && gemv_silu_ok(2 * I, D, y.gu_bits);
+    // (measured in the 40-layer step at ctx 2048: 2.98 ms against 3.03 ms
+    // with the 64-row-unit epilogue, whose 544 units cannot spread evenly
+    // over 256 CUs)
     if (silu_fused) {
-      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.y, 2 * I,
-                               D, y.gu_bits, st, true));
+      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu, 2 * I,
+                               D, y.gu_bits, st, SiluEpi::kPair));
+      prof.mark(st, kGemv);
+      R4Q_TRY(gemv_fwht_launch(reinterpret_cast<const float*>(bf.gu), y.down_w, y.down_s, bf.d,
+                               D, I, y.down_bits, st));
     } else {
       if (fused) {
         R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu,
@@ -213,9 +220,9 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
       }
       prof.mark(st, kNorm);
       R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
+      prof.mark(st, kGemv);
+      R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
     }
-    prof.mark(st, kGemv);
-    R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
     if (!fused) {
       prof.mark(st, kNorm);
       const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm : m->final_norm;

@@ -265,6 +265,45 @@ __device__ __forceinline__ void stage_x_norm(const uint16_t* __restrict__ x, con
   __syncthreads();
 }
 
+// Activation of the down projection after the split SiLU-gate epilogue:
+// x = fp16(FWHT32(h)) per 32-element chunk from the fp32 products h, with
+// the butterflies, scaling and rounding of silu_kernel<true> (fwht32,
+// store32h), so the staged activation is bit-identical to that kernel's
+// output.
+template <int WBITS>
+__device__ __forceinline__ void stage_x_fwht(const float* __restrict__ h, uint32_t* xs, int K) {
+  constexpr int E = Fmt<WBITS>::kElems;
+  constexpr int XD = Fmt<WBITS>::kXDw;
+  for (int c = threadIdx.x; c < K / 32; c += blockDim.x) {
+    const f4_t* src = reinterpret_cast<const f4_t*>(h + (int64_t)c * 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f4_t q = src[i];
+      v[4 * i] = q[0];
+      v[4 * i + 1] = q[1];
+      v[4 * i + 2] = q[2];
+      v[4 * i + 3] = q[3];
+    }
+    fwht32(v);
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      raw[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
+#pragma unroll
+    for (int sub = 0; sub < 32 / E; ++sub)
+      prep_raw<WBITS>(raw + sub * (E / 2), xs + (c * (32 / E) + sub) * XD);
+  }
+  __syncthreads();
+}
+
+// Input modes of the GEMV: x as fp16, the fused residual + RMSNorm + FWHT
+// of GemvNorm, or fp32 SiLU products through stage_x_fwht.
+constexpr int kXPlain = 0, kXNorm = 1, kXFwht = 2;
+// Epilogues: fp16 rows; the SiLU unit map (64-row units, fp16 FWHT32 of the
+// gated products); the SiLU pair map (fp32 gated products, no FWHT).
+constexpr int kEpiRows = 0, kEpiSiluUnit = 1, kEpiSiluPair = 2;
+
 template <int WBITS>
 __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, int c) {
   if constexpr (WBITS == 4) return srow[c];
@@ -286,23 +325,30 @@ struct GemvTile {
   uint32_t s2[UB][CPL];
 };
 
-// Linear map: workgroup g takes global steps g, g + G, ...  SiLU map (gate /
-// up halves of a [2I] output): a unit is 32 gate rows and the 32 up rows of
-// the same indices; workgroup g takes units g, g + G, ..., each as SPU
-// consecutive steps (gate rows first).
-template <int RPS, bool SILU>
+// Linear map: workgroup g takes global steps g, g + G, ...  SiLU unit map
+// (gate / up halves of a [2I] output): a unit is 32 gate rows and the 32 up
+// rows of the same indices; workgroup g takes units g, g + G, ..., each as
+// SPU consecutive steps (gate rows first).  SiLU pair map: a pair step is RPS
+// gate rows and the RPS up rows of the same indices, taken as two
+// consecutive local steps (gate, then up) by the same lanes; workgroup g
+// takes pair steps g, g + G, ...
+template <int RPS, int EPI>
 struct RowMap {
   int g, G, nsteps;  // linear
-  int I, nunits;     // SiLU: I = N / 2, nunits = I / 32
+  int I, nunits;     // SiLU: I = N / 2, nunits = I / 32 (unit) or I / RPS (pair)
   static constexpr int SPU = 64 / RPS;
   __device__ int nlocal() const {
-    if constexpr (SILU) return g < nunits ? ((nunits - g + G - 1) / G) * SPU : 0;
+    if constexpr (EPI == kEpiSiluUnit) return g < nunits ? ((nunits - g + G - 1) / G) * SPU : 0;
+    else if constexpr (EPI == kEpiSiluPair) return g < nunits ? ((nunits - g + G - 1) / G) * 2 : 0;
     else return g < nsteps ? (nsteps - g + G - 1) / G : 0;
   }
   __device__ int row0(int k) const {
-    if constexpr (SILU) {
+    if constexpr (EPI == kEpiSiluUnit) {
       const int u = g + G * (k / SPU), sub = k % SPU;
       return sub < SPU / 2 ? 32 * u + RPS * sub : I + 32 * u + RPS * (sub - SPU / 2);
+    } else if constexpr (EPI == kEpiSiluPair) {
+      const int ps = g + G * (k >> 1);
+      return (k & 1) ? I + RPS * ps : RPS * ps;
     } else {
       return (g + G * k) * RPS;
     }
@@ -348,19 +394,37 @@ __device__ __forceinline__ void silu_unit(const float* ut, uint16_t* __restrict_
   if (threadIdx.x < 32) y[32 * u + i] = f2h(v);
 }
 
+// silu(g) * u as silu_kernel computes it (separately rounded fp32 steps).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.0f + expf(-g)) * u;
+}
+
 // Finishes step k (the k-th of this workgroup) from the lane partials
 // `acc`.  Rows spread over several waves leave one partial per (step, wave)
 // in `red`; they are combined once, after the last step.  In the SiLU map
 // each row's fp16-rounded result goes to the unit buffer `ut`, and the
-// unit's last step writes its 32 outputs.
-template <int LPR, class Map, bool SILU>
+// unit's last step writes its 32 outputs.  In the SiLU pair map the gate
+// step parks each row's fp16-rounded value in ut[row slot] (the same lane
+// reads it back), and the up step writes silu(g) * u as fp32.
+template <int LPR, class Map, int EPI>
 __device__ __forceinline__ void gemv_finish(float acc, uint16_t* __restrict__ y, float* red,
                                             float* ut, int N, const Map& map, int k, int rs,
                                             int cl) {
   constexpr int RPS = 256 / LPR;
   if constexpr (LPR <= 64) {
     const float total = reduce_lr(acc, LPR);
-    if constexpr (SILU) {
+    if constexpr (EPI == kEpiSiluPair) {
+      if (cl == 0) {
+        const float v = h2f(f2h(total));
+        if ((k & 1) == 0) {
+          ut[rs] = v;
+        } else {
+          const int row = map.row0(k) - map.I + rs;
+          reinterpret_cast<float*>(y)[row] = silu_mul(ut[rs], v);
+        }
+      }
+    } else if constexpr (EPI == kEpiSiluUnit) {
       constexpr int SPU = Map::SPU;
       const int sub = k % SPU;
       const int slot = (k / SPU) & 1;
@@ -381,7 +445,7 @@ __device__ __forceinline__ void gemv_finish(float acc, uint16_t* __restrict__ y,
 }
 
 // Computes the UB steps of a batch.
-template <int WBITS, int LPR, int CPL, int UB, class Map, bool SILU>
+template <int WBITS, int LPR, int CPL, int UB, class Map, int EPI>
 __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>& t,
                                              const uint32_t* __restrict__ xr,
                                              uint16_t* __restrict__ y, float* red, float* ut,
@@ -398,7 +462,7 @@ __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>
       if (LPR * CPL <= cpr || cl + LPR * i < cpr)
         acc = chunk_dot<WBITS>(t.wq[j][i], t.s2[j][i], xr + i * XD, acc);
     }
-    gemv_finish<LPR, Map, SILU>(acc, y, red, ut, N, map, k, rs, cl);
+    gemv_finish<LPR, Map, EPI>(acc, y, red, ut, N, map, k, rs, cl);
   }
 }
 
@@ -406,7 +470,7 @@ __device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>
 // consumed, its register is refilled with chunk i of step k + 1, so the next
 // step's loads overlap this step's arithmetic while no lane holds more than
 // one step's chunks in flight.
-template <int WBITS, int LPR, int CPL, class Map, bool SILU, bool NEXT>
+template <int WBITS, int LPR, int CPL, class Map, int EPI, bool NEXT>
 __device__ __forceinline__ void gemv_step_roll(GemvTile<WBITS, LPR, CPL, 1>& t,
                                                const uint32_t* __restrict__ xr,
                                                const uint8_t* __restrict__ w,
@@ -434,43 +498,45 @@ __device__ __forceinline__ void gemv_step_roll(GemvTile<WBITS, LPR, CPL, 1>& t,
       t.s2[0][i] = load_sz<WBITS>(srow, c);
     }
   }
-  gemv_finish<LPR, Map, SILU>(acc, y, red, ut, N, map, k, rs, cl);
+  gemv_finish<LPR, Map, EPI>(acc, y, red, ut, N, map, k, rs, cl);
 }
 
 // Main-loop schedule: rolling prefetch (one step per iteration) when true,
 // else load-then-compute batches of UB steps.
 constexpr bool kRollingPrefetch = true;
 
-template <int WBITS, int LPR, int CPL, int UB, bool NORM, bool SILU>
+template <int WBITS, int LPR, int CPL, int UB, int XM, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x,
                                                    const uint8_t* __restrict__ w,
                                                    const uint32_t* __restrict__ sz,
                                                    uint16_t* __restrict__ y, int N, int K,
                                                    GemvNorm nm) {
-  static_assert(!SILU || LPR <= 64, "the SiLU epilogue needs rows inside one wave");
+  static_assert(EPI == kEpiRows || LPR <= 64, "the SiLU epilogues need rows inside one wave");
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int RPS = 256 / LPR;
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;  // waves per row
   extern __shared__ __align__(16) uint32_t xs[];
-  __shared__ float ut[SILU ? 128 : 1];
+  __shared__ float ut[EPI == kEpiSiluUnit ? 128 : EPI == kEpiSiluPair ? RPS : 1];
   const int cpr = K / Fmt<WBITS>::kElems;
   const int nb = K / 32;
   const int64_t row_bytes = (int64_t)K * WBITS / 8;
   const int rs = threadIdx.x / LPR, cl = threadIdx.x % LPR;
-  RowMap<RPS, SILU> map;
+  RowMap<RPS, EPI> map;
   map.g = blockIdx.x;
   map.G = gridDim.x;
   map.nsteps = (N + RPS - 1) / RPS;
   map.I = N / 2;
-  map.nunits = N / 64;
+  map.nunits = EPI == kEpiSiluPair ? N / (2 * RPS) : N / 64;
   const int nloc = map.nlocal();
 
   GemvTile<WBITS, LPR, CPL, UB> ta;
   if (nloc > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, 0, nloc, rs, cl);
 
-  if constexpr (NORM) {
+  if constexpr (XM == kXNorm) {
     __shared__ float nred[4];
     stage_x_norm<WBITS>(x, nm, xs, nred, K);
+  } else if constexpr (XM == kXFwht) {
+    stage_x_fwht<WBITS>(reinterpret_cast<const float*>(x), xs, K);
   } else {
     stage_x<WBITS>(x, xs, cpr);
   }
@@ -488,15 +554,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   // arithmetic (measured 11.9 -> 10.4 us for 17408 x 5120 INT4).
   if constexpr (kRollingPrefetch && UB == 1) {
     for (int k = 0; k + 1 < nloc; ++k)
-      gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, SILU>, SILU, true>(
+      gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, EPI>, EPI, true>(
           ta, xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, k, rs, cl);
     if (nloc > 0)
-      gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, SILU>, SILU, false>(
+      gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, EPI>, EPI, false>(
           ta, xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, nloc - 1, rs, cl);
   } else {
     for (int k = 0; k < nloc; k += UB) {
       if (k > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, k, nloc, rs, cl);
-      gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, SILU>, SILU>(ta, xr, y, red, ut, cpr, N,
+      gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, EPI>, EPI>(ta, xr, y, red, ut, cpr, N,
                                                                 map, k, nloc, rs, cl);
     }
   }
@@ -520,7 +586,7 @@ int env_int(const char* name, int dflt) {
 
 template <int WBITS>
 int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
-                    const GemvNorm* norm, bool silu, hipStream_t st) {
+                    const GemvNorm* norm, int xm, int epi, hipStream_t st) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
   constexpr int kCpl = Fmt<WBITS>::kCpl;
@@ -535,19 +601,25 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   lpr = env_int("R4Q_GEMV_LPR", lpr);
   R4Q_REQUIRE(lpr * kCpl >= cpr, "gemv: K=%lld needs more than 256 lanes per row", (long long)K);
   const int rps = 256 / lpr;
-  if (silu)
+  if (epi != kEpiRows)
     R4Q_REQUIRE(lpr <= 64 && N % 64 == 0,
                 "gemv: SiLU epilogue needs N %% 64 == 0 and rows inside a wave");
-  // SiLU: work items are units of 64 rows (steps counted per unit)
-  const int64_t nsteps = silu ? N / 64 : (N + rps - 1) / rps;
+  // work items: steps of rps rows; SiLU unit map: units of 64 rows; SiLU
+  // pair map: pair steps (rps gate rows + their rps up rows)
+  const int64_t nsteps = epi == kEpiSiluUnit   ? N / 64
+                         : epi == kEpiSiluPair ? N / (2 * rps)
+                                               : (N + rps - 1) / rps;
   // Workgroups: about the resident capacity (measured best: 4 per CU for
   // rows inside one wave, 2-3 per CU for rows spread over waves), with an
   // equal number of steps each.  A fused-norm prologue is paid once per
   // workgroup and the workgroups of a CU compute it on the same SIMDs: at
   // most one per CU (measured 9.1 -> 8.2 us for 7168 x 5120 INT4), except
-  // in the SiLU map, whose 64-row units need one workgroup each.
-  const int max_wg = env_int("R4Q_GEMV_WGS", norm ? (lpr == 128 ? 512 : silu ? 768 : 256)
-                                                  : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768));
+  // in the SiLU maps: the unit map needs one workgroup per 64-row unit, and
+  // the pair map measured best at 768.
+  const bool nrm = xm == kXNorm;
+  const int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : 256)
+                       : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
+  const int max_wg = env_int("R4Q_GEMV_WGS", dflt);
   const int ub = env_int("R4Q_GEMV_UB", 1);
   const int64_t per = (nsteps + max_wg - 1) / max_wg;
   const int64_t grid = (nsteps + per - 1) / per;
@@ -559,29 +631,34 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
-  if (norm) R4Q_REQUIRE(K <= 32 * 256, "gemv: fused norm needs K <= 8192 (K=%lld)", (long long)K);
+  if (nrm) R4Q_REQUIRE(K <= 32 * 256, "gemv: fused norm needs K <= 8192 (K=%lld)", (long long)K);
   const GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
-#define R4Q_GEMV_K(L, U, NRM, SIL)                                                         \
-  hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, NRM, SIL>), gd, bd, lds_all, st, xp, wp, sp, \
+#define R4Q_GEMV_K(L, U, XM, EPI)                                                             \
+  hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, XM, EPI>), gd, bd, lds_all, st, xp, wp, sp, \
                      yp, (int)N, (int)K, nm)
-  // rows inside one wave: plain, fused norm, SiLU epilogue, both
-#define R4Q_GEMV(L, U)                                                                      \
-  if (lpr == L && ub == U) {                                                                \
-    if (norm && silu) R4Q_GEMV_K(L, U, true, true);                                         \
-    else if (norm) R4Q_GEMV_K(L, U, true, false);                                           \
-    else if (silu) R4Q_GEMV_K(L, U, false, true);                                           \
-    else R4Q_GEMV_K(L, U, false, false);                                                    \
-    return launch_status("gemv");                                                           \
+  // rows inside one wave: every input mode; SiLU epilogues after the fp16
+  // or fused-norm input
+#define R4Q_GEMV(L, U)                                                                       \
+  if (lpr == L && ub == U) {                                                                 \
+    if (epi == kEpiSiluUnit && nrm) R4Q_GEMV_K(L, U, kXNorm, kEpiSiluUnit);                  \
+    else if (epi == kEpiSiluUnit) R4Q_GEMV_K(L, U, kXPlain, kEpiSiluUnit);                   \
+    else if (epi == kEpiSiluPair && nrm) R4Q_GEMV_K(L, U, kXNorm, kEpiSiluPair);             \
+    else if (epi == kEpiSiluPair) R4Q_GEMV_K(L, U, kXPlain, kEpiSiluPair);                   \
+    else if (nrm) R4Q_GEMV_K(L, U, kXNorm, kEpiRows);                                        \
+    else if (xm == kXFwht) R4Q_GEMV_K(L, U, kXFwht, kEpiRows);                               \
+    else R4Q_GEMV_K(L, U, kXPlain, kEpiRows);                                                \
+    return launch_status("gemv");                                                            \
   }
   R4Q_GEMV(16, 1) R4Q_GEMV(32, 1) R4Q_GEMV(64, 1)
   R4Q_GEMV(16, 2) R4Q_GEMV(32, 2) R4Q_GEMV(64, 2)
 #undef R4Q_GEMV
-  // rows over 2 or 4 waves: plain or fused norm
-#define R4Q_GEMV(L, U)                                                                      \
-  if (lpr == L && ub == U) {                                                                \
-    if (norm) R4Q_GEMV_K(L, U, true, false);                                                \
-    else R4Q_GEMV_K(L, U, false, false);                                                    \
-    return launch_status("gemv");                                                           \
+  // rows over 2 or 4 waves: fp16 rows from every input mode
+#define R4Q_GEMV(L, U)                                                                       \
+  if (lpr == L && ub == U) {                                                                 \
+    if (nrm) R4Q_GEMV_K(L, U, kXNorm, kEpiRows);                                             \
+    else if (xm == kXFwht) R4Q_GEMV_K(L, U, kXFwht, kEpiRows);                               \
+    else R4Q_GEMV_K(L, U, kXPlain, kEpiRows);                                                \
+    return launch_status("gemv");                                                            \
   }
   R4Q_GEMV(128, 1) R4Q_GEMV(256, 1) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
 #undef R4Q_GEMV
@@ -611,23 +688,36 @@ int gemv_check(const void* x, const void* w, const void* sz, const void* y, int6
 int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                 int wbits, hipStream_t st) {
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, nullptr, false, st);
-    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, nullptr, false, st);
-    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, nullptr, false, st);
+    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, nullptr, kXPlain, kEpiRows, st);
+    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, nullptr, kXPlain, kEpiRows, st);
+    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, nullptr, kXPlain, kEpiRows, st);
   }
 }
 
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st, bool silu) {
+                     hipStream_t st, SiluEpi silu) {
   R4Q_REQUIRE(a && (!b || (gamma && res_out)), "gemv_norm: null pointer");
   const GemvNorm nm{static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(gamma),
                     static_cast<uint16_t*>(res_out), eps};
   const GemvNorm* np = gamma ? &nm : nullptr;
+  const int xm = gamma ? kXNorm : kXPlain;
+  const int epi = silu == SiluEpi::kNone   ? kEpiRows
+                  : silu == SiluEpi::kUnit ? kEpiSiluUnit
+                                           : kEpiSiluPair;
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, np, silu, st);
-    case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, np, silu, st);
-    default: return launch_gemv_fmt<16>(a, w, sz, y, N, K, np, silu, st);
+    case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, np, xm, epi, st);
+    case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, np, xm, epi, st);
+    default: return launch_gemv_fmt<16>(a, w, sz, y, N, K, np, xm, epi, st);
+  }
+}
+
+int gemv_fwht_launch(const float* h, const void* w, const void* sz, void* y, int64_t N,
+                     int64_t K, int wbits, hipStream_t st) {
+  switch (wbits) {
+    case 4: return launch_gemv_fmt<4>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
+    case 8: return launch_gemv_fmt<8>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
+    default: return launch_gemv_fmt<16>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
   }
 }
 
@@ -708,5 +798,30 @@ extern "C" int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* g
                   (reinterpret_cast<uintptr_t>(res_out) & 15) == 0,
               "gate_up_silu_fwht: pointers must be 16-byte aligned");
   return r4q::gemv_norm_launch(a, gamma ? b : nullptr, gamma, gamma ? res_out : nullptr, eps, w,
-                               sz, y, 2 * I, K, wbits, r4q::as_stream(stream), true);
+                               sz, y, 2 * I, K, wbits, r4q::as_stream(stream),
+                               r4q::SiluEpi::kUnit);
+}
+
+extern "C" int r4q_gate_up_silu(const void* a, const void* b, const void* gamma, void* res_out,
+                                float eps, const void* w, const void* sz, float* h, int64_t I,
+                                int64_t K, int wbits, void* stream) {
+  R4Q_REQUIRE(I > 0 && I % 32 == 0, "gate_up_silu: I must be a positive multiple of 32");
+  R4Q_TRY(r4q::gemv_check(a, w, sz, h, 2 * I, K, wbits));
+  R4Q_REQUIRE(wbits != 16 && r4q::gemv_silu_ok(2 * I, K, wbits),
+              "gate_up_silu: INT4 / INT8 rows of at most 320 chunks only");
+  R4Q_REQUIRE(!gamma || !b || res_out, "gate_up_silu: residual output required");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(gamma) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(res_out) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(h) & 3) == 0,
+              "gate_up_silu: pointers must be aligned (16 bytes; h: 4)");
+  return r4q::gemv_norm_launch(a, gamma ? b : nullptr, gamma, gamma ? res_out : nullptr, eps, w,
+                               sz, h, 2 * I, K, wbits, r4q::as_stream(stream),
+                               r4q::SiluEpi::kPair);
+}
+
+extern "C" int r4q_fwht_gemv(const float* h, const void* w, const void* sz, void* y, int64_t N,
+                             int64_t K, int wbits, void* stream) {
+  R4Q_TRY(r4q::gemv_check(h, w, sz, y, N, K, wbits));
+  return r4q::gemv_fwht_launch(h, w, sz, y, N, K, wbits, r4q::as_stream(stream));
 }

@@ -16,13 +16,22 @@ int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N
 // y = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) computed in the
 // GEMV's activation staging (residual + RMSNorm + FWHT-32 fused); workgroup 0
 // writes res_out = fp16(a + b) when b != NULL.  gamma == NULL: plain x = a.
-// K <= 8192 with a norm, batch 1.  silu: W's rows are [gate; up] (N = 2I)
-// and y[I] = fp16(FWHT32(silu(g) * u)) of the fp16-rounded rows (the
-// SiLU-gate kernel fused into the epilogue); needs gemv_silu_ok(N, K, wbits).
+// K <= 8192 with a norm, batch 1.  silu (W's rows [gate; up], N = 2I, g and
+// u the fp16-rounded rows; needs gemv_silu_ok(N, K, wbits)):
+//   kUnit: y[I] = fp16(FWHT32(silu(g) * u)), the SiLU-gate kernel fused
+//          into the epilogue (one workgroup per 64-row unit);
+//   kPair: y[I] = silu(g) * u as fp32 (float*), no FWHT: gemv_fwht_launch
+//          applies it in the next GEMV's staging (any grid size).
+enum class SiluEpi { kNone, kUnit, kPair };
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st, bool silu = false);
+                     hipStream_t st, SiluEpi silu = SiluEpi::kNone);
 bool gemv_silu_ok(int64_t N, int64_t K, int wbits);
+// y = W x with x = fp16(FWHT32(h)) per 32 elements from fp32 h (K % 32 == 0):
+// the down projection after a kPair gate/up GEMV, x bit-identical to the
+// SiLU-gate kernel's output.
+int gemv_fwht_launch(const float* h, const void* w, const void* sz, void* y, int64_t N,
+                     int64_t K, int wbits, hipStream_t st);
 
 // Row counts up to this use the weight-streaming GEMV path; above it the
 // MFMA tile GEMM with on-the-fly dequantisation.

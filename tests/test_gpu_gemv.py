@@ -182,3 +182,57 @@ def test_gate_up_silu_fwht_bit_exact(dev, bits, I, K, norm):
     # and against the oracle (its exp is numpy's: last-bit differences)
     want = O.silu_mul_fwht(gu[:I].cpu().numpy(), gu[I:].cpu().numpy())
     assert rel_l2(y2.cpu().numpy(), want) <= 1e-3
+
+
+@pytest.mark.parametrize("bits,dbits", [(4, 4), (8, 8), (4, 16)])
+@pytest.mark.parametrize("I,K,norm", [(17408, 5120, True), (1024, 5120, False), (96, 256, True),
+                                      (64, 2048, False)])
+def test_gate_up_silu_pair_then_fwht_gemv_bit_exact(dev, bits, dbits, I, K, norm):
+    """r4q_gate_up_silu (fp32 silu(g) * u) followed by r4q_fwht_gemv (FWHT-32
+    in the staging) == r4q_gate_up_silu_fwht followed by r4q_gemv, bit for bit
+    on the down projection's output and the residual output; h itself against
+    the oracle's SiLU product of the GEMV rows."""
+    import r4q_lib as R
+    g = S.gen(7 * I + K + bits + dbits)
+    w, sz = (t.to(dev) for t in S.weight(2 * I, K, bits, g))
+    N = K  # the down projection maps back to the hidden size
+    wd, szd = S.weight(N, I, dbits, g)
+    wd = wd.to(dev)
+    szd = None if szd is None else szd.to(dev)
+    a = (torch.randn(K, generator=g) * 0.7).half().to(dev)
+    b = (torch.randn(K, generator=g) * 0.7).half().to(dev)
+    gam = S.norm_weight(K, g).to(dev)
+    eps = 1e-6
+    y16 = torch.empty(I, dtype=torch.float16, device=dev)
+    h = torch.full((I,), float("nan"), dtype=torch.float32, device=dev)
+    gu = torch.empty(2 * I, dtype=torch.float16, device=dev)
+    d1 = torch.empty(N, dtype=torch.float16, device=dev)
+    d2 = torch.empty(N, dtype=torch.float16, device=dev)
+    res1 = torch.empty(K, dtype=torch.float16, device=dev)
+    res2 = torch.zeros(K, dtype=torch.float16, device=dev)
+    st = R.stream_handle()
+    szp = None if szd is None else szd.data_ptr()
+    if norm:
+        R.call("r4q_gate_up_silu_fwht", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
+               res1.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), y16.data_ptr(), I, K, bits, st)
+        R.call("r4q_gate_up_silu", a.data_ptr(), b.data_ptr(), gam.data_ptr(), res2.data_ptr(),
+               eps, w.data_ptr(), sz.data_ptr(), h.data_ptr(), I, K, bits, st)
+        R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
+               res1.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K, bits, st)
+    else:
+        R.call("r4q_gate_up_silu_fwht", a.data_ptr(), None, None, None, eps, w.data_ptr(),
+               sz.data_ptr(), y16.data_ptr(), I, K, bits, st)
+        R.call("r4q_gate_up_silu", a.data_ptr(), None, None, None, eps, w.data_ptr(),
+               sz.data_ptr(), h.data_ptr(), I, K, bits, st)
+        R.call("r4q_gemv", a.data_ptr(), w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K,
+               bits, st)
+    R.call("r4q_gemv", y16.data_ptr(), wd.data_ptr(), szp, d1.data_ptr(), N, I, dbits, st)
+    R.call("r4q_fwht_gemv", h.data_ptr(), wd.data_ptr(), szp, d2.data_ptr(), N, I, dbits, st)
+    torch.cuda.synchronize()
+    assert torch.isfinite(h).all()
+    assert torch.equal(d1.view(torch.int16), d2.view(torch.int16))
+    if norm:
+        assert torch.equal(res1.view(torch.int16), res2.view(torch.int16))
+    # the oracle rounds the product to fp16 (and its exp is numpy's)
+    want = O.silu_mul(gu[:I].cpu().numpy(), gu[I:].cpu().numpy())
+    assert rel_l2(h.cpu().numpy(), want) <= 1e-3
