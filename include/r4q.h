@@ -139,20 +139,26 @@ R4Q_API int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* gamm
                           void* res_out, float eps, const void* w, const void* sz,
                           void* y, int64_t I, int64_t K, int wbits, void* stream);
 
-/* The same pair split at the FWHT, as the decode step runs it: r4q_gate_up_silu
- * writes h[I] = silu(fp16(g)) * fp16(u) as fp32 (arguments as
- * r4q_gate_up_silu_fwht, h 4-byte aligned), and r4q_fwht_gemv computes
- * y = W x with x = fp16(FWHT32(h)) per 32 elements (K % 32 == 0), x
- * bit-identical to r4q_silu_mul_fwht's output, so y equals r4q_gemv of that
- * output.  Gate and up rows of the same index are reduced by the same lanes,
- * so no workgroup has to own 64-row units and the grid size is free.
+/* The same pair split at a point, as the decode step runs it.
+ * r4q_gate_up_silu writes y[i] = fp16(FWHT32(silu(fp16(g)) * fp16(u)))[i]
+ * for i < split (fp16, as r4q_gate_up_silu_fwht) and h[i] = silu(fp16(g_i)) *
+ * fp16(u_i) as fp32 for i >= split (no FWHT); split is a multiple of 32 in
+ * [0, I], y and h are [I] arrays (only their own part is written; h 16-byte
+ * aligned).  r4q_fwht_gemv computes y = W x with x[i] = x16[i] below split
+ * and x = fp16(FWHT32(h)) per 32 elements above it, so x is bit-identical
+ * to r4q_silu_mul_fwht's output and y to r4q_gemv of it.
+ * The elements below the split go in 64-row units (32 gate + 32 up rows,
+ * one workgroup each), the rest as pairs spread over every workgroup;
+ * r4q_gate_up_silu_split returns the split that keeps whole units in
+ * multiples of the CU count.
  * Replace the launch_gemv (gate_up) -> silu_hadamard_ds -> launch_gemv (down)
  * chain of the reference's decode step (hip:2508-2516). */
+R4Q_API int r4q_gate_up_silu_split(int64_t I, int64_t* split);
 R4Q_API int r4q_gate_up_silu(const void* a, const void* b, const void* gamma, void* res_out,
-                     float eps, const void* w, const void* sz, float* h, int64_t I,
-                     int64_t K, int wbits, void* stream);
-R4Q_API int r4q_fwht_gemv(const float* h, const void* w, const void* sz, void* y, int64_t N,
-                  int64_t K, int wbits, void* stream);
+                     float eps, const void* w, const void* sz, void* y, float* h,
+                     int64_t split, int64_t I, int64_t K, int wbits, void* stream);
+R4Q_API int r4q_fwht_gemv(const void* x16, const float* h, int64_t split, const void* w,
+                  const void* sz, void* y, int64_t N, int64_t K, int wbits, void* stream);
 
 /* ------------------------------------------------------ norms / rotations */
 

@@ -196,18 +196,21 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     prof.mark(st, kGemv);
     R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
     // gate/up: r = fp16(o + h), RMSNorm + FWHT in the staging and, for
-    // INT4/INT8, silu(g) * u in the epilogue as fp32 (in bf.gu, unused at
-    // batch 1); the down GEMV applies the FWHT-32 in its staging
+    // INT4/INT8, the SiLU-gate in the epilogue: fp16 FWHT'd output for the
+    // whole 64-row units below the split (a multiple of the CU count, one
+    // workgroup each), fp32 silu(g) * u above it (in bf.gu, unused at batch
+    // 1); the down GEMV applies the FWHT-32 to that part in its staging.
+    // (A unit map alone has 544 units for 256 CUs at I = 17408.)
     const bool silu_fused = fused && y.gu_bits != 16 && gemv_silu_ok(2 * I, D, y.gu_bits);
-    // (measured in the 40-layer step at ctx 2048: 2.98 ms against 3.03 ms
-    // with the 64-row-unit epilogue, whose 544 units cannot spread evenly
-    // over 256 CUs)
     if (silu_fused) {
-      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu, 2 * I,
-                               D, y.gu_bits, st, SiluEpi::kPair));
+      // (40-layer step, ctx 2048: 2.925 ms; every element as fp32 pairs:
+      // 2.99 ms; every element in units: 3.02 ms)
+      const int64_t split = gemv_silu_split(I);
+      float* hp = reinterpret_cast<float*>(bf.gu);
+      R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.y, 2 * I,
+                               D, y.gu_bits, st, SiluEpi::kSplit, hp, split));
       prof.mark(st, kGemv);
-      R4Q_TRY(gemv_fwht_launch(reinterpret_cast<const float*>(bf.gu), y.down_w, y.down_s, bf.d,
-                               D, I, y.down_bits, st));
+      R4Q_TRY(gemv_fwht_launch(bf.y, hp, split, y.down_w, y.down_s, bf.d, D, I, y.down_bits, st));
     } else {
       if (fused) {
         R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu,

@@ -229,6 +229,10 @@ struct GemvNorm {
   const uint16_t* gamma;  // [K] norm weight
   uint16_t* res_out;      // [K] fp16(x + b), when b != NULL
   float eps;
+  // SiLU split epilogue / mixed staging: fp32 products of elements
+  // [split, I) (indexed by element) and the split point (a multiple of 32)
+  float* h;
+  int split;
 };
 
 template <int WBITS>
@@ -266,15 +270,23 @@ __device__ __forceinline__ void stage_x_norm(const uint16_t* __restrict__ x, con
 }
 
 // Activation of the down projection after the split SiLU-gate epilogue:
-// x = fp16(FWHT32(h)) per 32-element chunk from the fp32 products h, with
-// the butterflies, scaling and rounding of silu_kernel<true> (fwht32,
-// store32h), so the staged activation is bit-identical to that kernel's
-// output.
+// elements below `split` are fp16 already (x); above it x = fp16(FWHT32(h))
+// per 32-element chunk from the fp32 products h, with the butterflies,
+// scaling and rounding of silu_kernel<true> (fwht32, store32h), so the
+// staged activation is bit-identical to that kernel's output.
 template <int WBITS>
-__device__ __forceinline__ void stage_x_fwht(const float* __restrict__ h, uint32_t* xs, int K) {
+__device__ __forceinline__ void stage_x_fwht(const uint16_t* __restrict__ x,
+                                             const float* __restrict__ h, int split, uint32_t* xs,
+                                             int K) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
   for (int c = threadIdx.x; c < K / 32; c += blockDim.x) {
+    if (32 * c < split) {
+#pragma unroll
+      for (int sub = 0; sub < 32 / E; ++sub)
+        prep_chunk<WBITS>(x, c * (32 / E) + sub, xs + (c * (32 / E) + sub) * XD);
+      continue;
+    }
     const f4_t* src = reinterpret_cast<const f4_t*>(h + (int64_t)c * 32);
     float v[32];
 #pragma unroll
@@ -301,7 +313,8 @@ __device__ __forceinline__ void stage_x_fwht(const float* __restrict__ h, uint32
 // of GemvNorm, or fp32 SiLU products through stage_x_fwht.
 constexpr int kXPlain = 0, kXNorm = 1, kXFwht = 2;
 // Epilogues: fp16 rows; the SiLU unit map (64-row units, fp16 FWHT32 of the
-// gated products); the SiLU pair map (fp32 gated products, no FWHT).
+// gated products); the SiLU split map (whole units first, then pairs of
+// the remaining rows as fp32 gated products, no FWHT).
 constexpr int kEpiRows = 0, kEpiSiluUnit = 1, kEpiSiluPair = 2;
 
 template <int WBITS>
@@ -328,18 +341,23 @@ struct GemvTile {
 // Linear map: workgroup g takes global steps g, g + G, ...  SiLU unit map
 // (gate / up halves of a [2I] output): a unit is 32 gate rows and the 32 up
 // rows of the same indices; workgroup g takes units g, g + G, ..., each as
-// SPU consecutive steps (gate rows first).  SiLU pair map: a pair step is RPS
+// SPU consecutive steps (gate rows first).  SiLU split map: workgroup g < F
+// first takes unit g as above; the rows from 32 F on go in pair steps of RPS
 // gate rows and the RPS up rows of the same indices, taken as two
 // consecutive local steps (gate, then up) by the same lanes; workgroup g
-// takes pair steps g, g + G, ...
+// takes pair steps g, g + G, ... of those.
 template <int RPS, int EPI>
 struct RowMap {
   int g, G, nsteps;  // linear
-  int I, nunits;     // SiLU: I = N / 2, nunits = I / 32 (unit) or I / RPS (pair)
+  int I, nunits;     // SiLU: I = N / 2; nunits = I / 32 (unit) or F (split)
+  int npairs;        // split: pair steps after the units
+  float* h;          // split: fp32 products, indexed by element
   static constexpr int SPU = 64 / RPS;
+  __device__ int nunit_steps() const { return g < nunits ? SPU : 0; }
   __device__ int nlocal() const {
     if constexpr (EPI == kEpiSiluUnit) return g < nunits ? ((nunits - g + G - 1) / G) * SPU : 0;
-    else if constexpr (EPI == kEpiSiluPair) return g < nunits ? ((nunits - g + G - 1) / G) * 2 : 0;
+    else if constexpr (EPI == kEpiSiluPair)
+      return nunit_steps() + (g < npairs ? ((npairs - g + G - 1) / G) * 2 : 0);
     else return g < nsteps ? (nsteps - g + G - 1) / G : 0;
   }
   __device__ int row0(int k) const {
@@ -347,8 +365,11 @@ struct RowMap {
       const int u = g + G * (k / SPU), sub = k % SPU;
       return sub < SPU / 2 ? 32 * u + RPS * sub : I + 32 * u + RPS * (sub - SPU / 2);
     } else if constexpr (EPI == kEpiSiluPair) {
-      const int ps = g + G * (k >> 1);
-      return (k & 1) ? I + RPS * ps : RPS * ps;
+      const int us = nunit_steps();
+      if (k < us) return k < SPU / 2 ? 32 * g + RPS * k : I + 32 * g + RPS * (k - SPU / 2);
+      const int kk = k - us;
+      const int p0 = 32 * nunits + RPS * (g + G * (kk >> 1));
+      return (kk & 1) ? I + p0 : p0;
     } else {
       return (g + G * k) * RPS;
     }
@@ -404,9 +425,10 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // `acc`.  Rows spread over several waves leave one partial per (step, wave)
 // in `red`; they are combined once, after the last step.  In the SiLU map
 // each row's fp16-rounded result goes to the unit buffer `ut`, and the
-// unit's last step writes its 32 outputs.  In the SiLU pair map the gate
-// step parks each row's fp16-rounded value in ut[row slot] (the same lane
-// reads it back), and the up step writes silu(g) * u as fp32.
+// unit's last step writes its 32 outputs.  In the pair steps of the SiLU
+// split map the gate step parks each row's fp16-rounded value in
+// ut[128 + row slot] (the same lane reads it back), and the up step writes
+// silu(g) * u as fp32 to h.
 template <int LPR, class Map, int EPI>
 __device__ __forceinline__ void gemv_finish(float acc, uint16_t* __restrict__ y, float* red,
                                             float* ut, int N, const Map& map, int k, int rs,
@@ -414,17 +436,17 @@ __device__ __forceinline__ void gemv_finish(float acc, uint16_t* __restrict__ y,
   constexpr int RPS = 256 / LPR;
   if constexpr (LPR <= 64) {
     const float total = reduce_lr(acc, LPR);
-    if constexpr (EPI == kEpiSiluPair) {
+    if (EPI == kEpiSiluPair && k >= map.nunit_steps()) {  // workgroup-uniform
       if (cl == 0) {
         const float v = h2f(f2h(total));
-        if ((k & 1) == 0) {
-          ut[rs] = v;
+        if (((k - map.nunit_steps()) & 1) == 0) {
+          ut[128 + rs] = v;
         } else {
           const int row = map.row0(k) - map.I + rs;
-          reinterpret_cast<float*>(y)[row] = silu_mul(ut[rs], v);
+          map.h[row] = silu_mul(ut[128 + rs], v);
         }
       }
-    } else if constexpr (EPI == kEpiSiluUnit) {
+    } else if constexpr (EPI == kEpiSiluUnit || EPI == kEpiSiluPair) {
       constexpr int SPU = Map::SPU;
       const int sub = k % SPU;
       const int slot = (k / SPU) & 1;
@@ -516,7 +538,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   constexpr int RPS = 256 / LPR;
   constexpr int WPR = LPR > 64 ? LPR / 64 : 1;  // waves per row
   extern __shared__ __align__(16) uint32_t xs[];
-  __shared__ float ut[EPI == kEpiSiluUnit ? 128 : EPI == kEpiSiluPair ? RPS : 1];
+  __shared__ float ut[EPI == kEpiSiluUnit ? 128 : EPI == kEpiSiluPair ? 128 + RPS : 1];
   const int cpr = K / Fmt<WBITS>::kElems;
   const int nb = K / 32;
   const int64_t row_bytes = (int64_t)K * WBITS / 8;
@@ -526,7 +548,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   map.G = gridDim.x;
   map.nsteps = (N + RPS - 1) / RPS;
   map.I = N / 2;
-  map.nunits = EPI == kEpiSiluPair ? N / (2 * RPS) : N / 64;
+  map.nunits = EPI == kEpiSiluPair ? nm.split / 32 : N / 64;
+  map.npairs = (N / 2 - nm.split) / RPS;
+  map.h = nm.h;
   const int nloc = map.nlocal();
 
   GemvTile<WBITS, LPR, CPL, UB> ta;
@@ -536,7 +560,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     __shared__ float nred[4];
     stage_x_norm<WBITS>(x, nm, xs, nred, K);
   } else if constexpr (XM == kXFwht) {
-    stage_x_fwht<WBITS>(reinterpret_cast<const float*>(x), xs, K);
+    stage_x_fwht<WBITS>(x, nm.h, nm.split, xs, K);
   } else {
     stage_x<WBITS>(x, xs, cpr);
   }
@@ -605,23 +629,26 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
     R4Q_REQUIRE(lpr <= 64 && N % 64 == 0,
                 "gemv: SiLU epilogue needs N %% 64 == 0 and rows inside a wave");
   // work items: steps of rps rows; SiLU unit map: units of 64 rows; SiLU
-  // pair map: pair steps (rps gate rows + their rps up rows)
+  // split map: one workgroup per whole unit below the split (F of them),
+  // else pair steps (rps gate rows + their rps up rows)
+  const int64_t F = epi == kEpiSiluPair ? norm->split / 32 : 0;
   const int64_t nsteps = epi == kEpiSiluUnit   ? N / 64
-                         : epi == kEpiSiluPair ? N / (2 * rps)
+                         : epi == kEpiSiluPair ? (F > 0 ? F : (N / 2 - norm->split) / rps)
                                                : (N + rps - 1) / rps;
   // Workgroups: about the resident capacity (measured best: 4 per CU for
   // rows inside one wave, 2-3 per CU for rows spread over waves), with an
   // equal number of steps each.  A fused-norm prologue is paid once per
   // workgroup and the workgroups of a CU compute it on the same SIMDs: at
   // most one per CU (measured 9.1 -> 8.2 us for 7168 x 5120 INT4), except
-  // in the SiLU maps: the unit map needs one workgroup per 64-row unit, and
-  // the pair map measured best at 768.
+  // in the SiLU maps: the unit map needs one workgroup per 64-row unit (as
+  // does the split map when it has units); pair steps alone measured best
+  // at 768.
   const bool nrm = xm == kXNorm;
   const int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : 256)
                        : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
   const int max_wg = env_int("R4Q_GEMV_WGS", dflt);
   const int ub = env_int("R4Q_GEMV_UB", 1);
-  const int64_t per = (nsteps + max_wg - 1) / max_wg;
+  const int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
   const int64_t grid = (nsteps + per - 1) / per;
   // the staging area also holds one partial per (step, wave) of the workgroup
   const size_t lds_all = lds > (size_t)per * 16 ? lds : (size_t)per * 16;
@@ -632,6 +659,10 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
   if (nrm) R4Q_REQUIRE(K <= 32 * 256, "gemv: fused norm needs K <= 8192 (K=%lld)", (long long)K);
+  if (xm == kXFwht)
+    R4Q_REQUIRE(norm && norm->split >= 0 && norm->split <= K && norm->split % 32 == 0 &&
+                    (norm->h || norm->split == K) && (x || norm->split == 0),
+                "gemv: bad FWHT staging split");
   const GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
 #define R4Q_GEMV_K(L, U, XM, EPI)                                                             \
   hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, XM, EPI>), gd, bd, lds_all, st, xp, wp, sp, \
@@ -696,15 +727,19 @@ int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N
 
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st, SiluEpi silu) {
+                     hipStream_t st, SiluEpi silu, float* h, int64_t split) {
   R4Q_REQUIRE(a && (!b || (gamma && res_out)), "gemv_norm: null pointer");
+  if (silu == SiluEpi::kSplit)
+    R4Q_REQUIRE(split >= 0 && split <= N / 2 && split % 32 == 0 && (h || split == N / 2) &&
+                    (y || split == 0),
+                "gemv_norm: bad SiLU split %lld", (long long)split);
   const GemvNorm nm{static_cast<const uint16_t*>(b), static_cast<const uint16_t*>(gamma),
-                    static_cast<uint16_t*>(res_out), eps};
-  const GemvNorm* np = gamma ? &nm : nullptr;
+                    static_cast<uint16_t*>(res_out), eps, h, (int)split};
+  const GemvNorm* np = (gamma || silu == SiluEpi::kSplit) ? &nm : nullptr;
   const int xm = gamma ? kXNorm : kXPlain;
   const int epi = silu == SiluEpi::kNone   ? kEpiRows
                   : silu == SiluEpi::kUnit ? kEpiSiluUnit
-                                           : kEpiSiluPair;
+                                           : kEpiSiluPair;  // kSplit
   switch (wbits) {
     case 4: return launch_gemv_fmt<4>(a, w, sz, y, N, K, np, xm, epi, st);
     case 8: return launch_gemv_fmt<8>(a, w, sz, y, N, K, np, xm, epi, st);
@@ -712,13 +747,21 @@ int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_
   }
 }
 
-int gemv_fwht_launch(const float* h, const void* w, const void* sz, void* y, int64_t N,
-                     int64_t K, int wbits, hipStream_t st) {
+int gemv_fwht_launch(const void* x, const float* h, int64_t split, const void* w,
+                     const void* sz, void* y, int64_t N, int64_t K, int wbits, hipStream_t st) {
+  const GemvNorm nm{nullptr, nullptr, nullptr, 0.f, const_cast<float*>(h), (int)split};
   switch (wbits) {
-    case 4: return launch_gemv_fmt<4>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
-    case 8: return launch_gemv_fmt<8>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
-    default: return launch_gemv_fmt<16>(h, w, sz, y, N, K, nullptr, kXFwht, kEpiRows, st);
+    case 4: return launch_gemv_fmt<4>(x, w, sz, y, N, K, &nm, kXFwht, kEpiRows, st);
+    case 8: return launch_gemv_fmt<8>(x, w, sz, y, N, K, &nm, kXFwht, kEpiRows, st);
+    default: return launch_gemv_fmt<16>(x, w, sz, y, N, K, &nm, kXFwht, kEpiRows, st);
   }
+}
+
+int64_t gemv_silu_split(int64_t I) {
+  // whole 64-row units in multiples of the 256 CUs (every CU gets the same
+  // number), the rest as pair steps spread over all workgroups
+  const int64_t units = I / 32;
+  return 32 * (units >= 256 ? units - units % 256 : units);
 }
 
 bool gemv_silu_ok(int64_t N, int64_t K, int wbits) {
@@ -802,26 +845,43 @@ extern "C" int r4q_gate_up_silu_fwht(const void* a, const void* b, const void* g
                                r4q::SiluEpi::kUnit);
 }
 
+extern "C" int r4q_gate_up_silu_split(int64_t I, int64_t* split) {
+  R4Q_REQUIRE(split && I > 0 && I % 32 == 0, "gate_up_silu_split: need I %% 32 == 0 and a result");
+  *split = r4q::gemv_silu_split(I);
+  return R4Q_OK;
+}
+
 extern "C" int r4q_gate_up_silu(const void* a, const void* b, const void* gamma, void* res_out,
-                                float eps, const void* w, const void* sz, float* h, int64_t I,
-                                int64_t K, int wbits, void* stream) {
+                                float eps, const void* w, const void* sz, void* y, float* h,
+                                int64_t split, int64_t I, int64_t K, int wbits, void* stream) {
   R4Q_REQUIRE(I > 0 && I % 32 == 0, "gate_up_silu: I must be a positive multiple of 32");
-  R4Q_TRY(r4q::gemv_check(a, w, sz, h, 2 * I, K, wbits));
+  R4Q_REQUIRE(split >= 0 && split <= I && split % 32 == 0,
+              "gate_up_silu: split must be a multiple of 32 in [0, I] (got %lld)", (long long)split);
+  R4Q_REQUIRE((split == 0 || y) && (split == I || h), "gate_up_silu: null output");
+  R4Q_TRY(r4q::gemv_check(a, w, sz, split > 0 ? y : static_cast<void*>(h), 2 * I, K, wbits));
   R4Q_REQUIRE(wbits != 16 && r4q::gemv_silu_ok(2 * I, K, wbits),
               "gate_up_silu: INT4 / INT8 rows of at most 320 chunks only");
   R4Q_REQUIRE(!gamma || !b || res_out, "gate_up_silu: residual output required");
   R4Q_REQUIRE((reinterpret_cast<uintptr_t>(gamma) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(b) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(res_out) & 15) == 0 &&
-                  (reinterpret_cast<uintptr_t>(h) & 3) == 0,
-              "gate_up_silu: pointers must be aligned (16 bytes; h: 4)");
+                  (reinterpret_cast<uintptr_t>(h) & 3) == 0 &&
+                  (reinterpret_cast<uintptr_t>(y) & 1) == 0,
+              "gate_up_silu: pointers must be aligned (16 bytes; h: 4; y: 2)");
   return r4q::gemv_norm_launch(a, gamma ? b : nullptr, gamma, gamma ? res_out : nullptr, eps, w,
-                               sz, h, 2 * I, K, wbits, r4q::as_stream(stream),
-                               r4q::SiluEpi::kPair);
+                               sz, y, 2 * I, K, wbits, r4q::as_stream(stream),
+                               r4q::SiluEpi::kSplit, h, split);
 }
 
-extern "C" int r4q_fwht_gemv(const float* h, const void* w, const void* sz, void* y, int64_t N,
-                             int64_t K, int wbits, void* stream) {
-  R4Q_TRY(r4q::gemv_check(h, w, sz, y, N, K, wbits));
-  return r4q::gemv_fwht_launch(h, w, sz, y, N, K, wbits, r4q::as_stream(stream));
+extern "C" int r4q_fwht_gemv(const void* x, const float* h, int64_t split, const void* w,
+                             const void* sz, void* y, int64_t N, int64_t K, int wbits,
+                             void* stream) {
+  R4Q_REQUIRE(split >= 0 && split <= K && split % 32 == 0,
+              "fwht_gemv: split must be a multiple of 32 in [0, K] (got %lld)", (long long)split);
+  R4Q_REQUIRE((split == 0 || x) && (split == K || h), "fwht_gemv: null input");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(h) & 15) == 0,
+              "fwht_gemv: x and h must be 16-byte aligned");
+  R4Q_TRY(r4q::gemv_check(split > 0 ? x : static_cast<const void*>(h), w, sz, y, N, K, wbits));
+  return r4q::gemv_fwht_launch(x, h, split, w, sz, y, N, K, wbits, r4q::as_stream(stream));
 }

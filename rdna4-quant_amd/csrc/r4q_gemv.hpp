@@ -18,20 +18,25 @@ int gemv_launch(const void* x, const void* w, const void* sz, void* y, int64_t N
 // writes res_out = fp16(a + b) when b != NULL.  gamma == NULL: plain x = a.
 // K <= 8192 with a norm, batch 1.  silu (W's rows [gate; up], N = 2I, g and
 // u the fp16-rounded rows; needs gemv_silu_ok(N, K, wbits)):
-//   kUnit: y[I] = fp16(FWHT32(silu(g) * u)), the SiLU-gate kernel fused
-//          into the epilogue (one workgroup per 64-row unit);
-//   kPair: y[I] = silu(g) * u as fp32 (float*), no FWHT: gemv_fwht_launch
-//          applies it in the next GEMV's staging (any grid size).
-enum class SiluEpi { kNone, kUnit, kPair };
+//   kUnit:  y[I] = fp16(FWHT32(silu(g) * u)), the SiLU-gate kernel fused
+//           into the epilogue (one workgroup per 64-row unit);
+//   kSplit: the same for elements [0, split) (one workgroup per 64-row unit,
+//           split / 32 of them), and h[i] = silu(g_i) * u_i as fp32 for
+//           i >= split, without the FWHT: gemv_fwht_launch applies it in the
+//           next GEMV's staging.  gemv_silu_split() gives a split whose
+//           units spread evenly over the CUs.
+enum class SiluEpi { kNone, kUnit, kSplit };
 int gemv_norm_launch(const void* a, const void* b, const void* gamma, void* res_out, float eps,
                      const void* w, const void* sz, void* y, int64_t N, int64_t K, int wbits,
-                     hipStream_t st, SiluEpi silu = SiluEpi::kNone);
+                     hipStream_t st, SiluEpi silu = SiluEpi::kNone, float* h = nullptr,
+                     int64_t split = 0);
 bool gemv_silu_ok(int64_t N, int64_t K, int wbits);
-// y = W x with x = fp16(FWHT32(h)) per 32 elements from fp32 h (K % 32 == 0):
-// the down projection after a kPair gate/up GEMV, x bit-identical to the
-// SiLU-gate kernel's output.
-int gemv_fwht_launch(const float* h, const void* w, const void* sz, void* y, int64_t N,
-                     int64_t K, int wbits, hipStream_t st);
+int64_t gemv_silu_split(int64_t I);
+// y = W x with x[i] = x16[i] for i < split and fp16(FWHT32(h)) per 32
+// elements above (K % 32 == 0): the down projection after a kSplit gate/up
+// GEMV, x bit-identical to the SiLU-gate kernel's output.
+int gemv_fwht_launch(const void* x16, const float* h, int64_t split, const void* w,
+                     const void* sz, void* y, int64_t N, int64_t K, int wbits, hipStream_t st);
 
 // Row counts up to this use the weight-streaming GEMV path; above it the
 // MFMA tile GEMM with on-the-fly dequantisation.

@@ -83,8 +83,9 @@ SIGNATURES = {
                               _i64, _i64, _i64, _i64, _f32, _i64, _i64, _p],
     "r4q_res_rmsnorm_fwht_gemv": [_p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i64, C.c_int, _p],
     "r4q_gate_up_silu_fwht": [_p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i64, C.c_int, _p],
-    "r4q_gate_up_silu": [_p, _p, _p, _p, _f32, _p, _p, _p, _i64, _i64, C.c_int, _p],
-    "r4q_fwht_gemv": [_p, _p, _p, _p, _i64, _i64, C.c_int, _p],
+    "r4q_gate_up_silu_split": [_i64, C.POINTER(_i64)],
+    "r4q_gate_up_silu": [_p, _p, _p, _p, _f32, _p, _p, _p, _p, _i64, _i64, _i64, C.c_int, _p],
+    "r4q_fwht_gemv": [_p, _p, _i64, _p, _p, _p, _i64, _i64, C.c_int, _p],
     "r4q_ctx_create": [C.POINTER(_p)],
     "r4q_ctx_destroy": [_p],
     "r4q_flash_decode": [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,

@@ -186,13 +186,22 @@ def test_gate_up_silu_fwht_bit_exact(dev, bits, I, K, norm):
 
 @pytest.mark.parametrize("bits,dbits", [(4, 4), (8, 8), (4, 16)])
 @pytest.mark.parametrize("I,K,norm", [(17408, 5120, True), (1024, 5120, False), (96, 256, True),
-                                      (64, 2048, False)])
-def test_gate_up_silu_pair_then_fwht_gemv_bit_exact(dev, bits, dbits, I, K, norm):
-    """r4q_gate_up_silu (fp32 silu(g) * u) followed by r4q_fwht_gemv (FWHT-32
-    in the staging) == r4q_gate_up_silu_fwht followed by r4q_gemv, bit for bit
-    on the down projection's output and the residual output; h itself against
-    the oracle's SiLU product of the GEMV rows."""
+                                      (8448, 2048, False)])
+@pytest.mark.parametrize("where", ["lib", "none", "all", "mid"])
+def test_gate_up_silu_split_then_fwht_gemv_bit_exact(dev, bits, dbits, I, K, norm, where):
+    """r4q_gate_up_silu (fp16 FWHT'd units below the split, fp32 silu(g) * u
+    above it) followed by r4q_fwht_gemv (FWHT-32 of the fp32 part in the
+    staging) == r4q_gate_up_silu_fwht followed by r4q_gemv, bit for bit on
+    the fp16 part, the down projection's output and the residual output;
+    the fp32 part against the oracle's SiLU product of the GEMV rows."""
+    import ctypes as C
     import r4q_lib as R
+    if where == "lib":
+        sp = C.c_int64()
+        R.call("r4q_gate_up_silu_split", I, C.byref(sp))
+        split = sp.value
+    else:
+        split = {"none": 0, "all": I, "mid": 32 * (I // 64)}[where]
     g = S.gen(7 * I + K + bits + dbits)
     w, sz = (t.to(dev) for t in S.weight(2 * I, K, bits, g))
     N = K  # the down projection maps back to the hidden size
@@ -204,6 +213,7 @@ def test_gate_up_silu_pair_then_fwht_gemv_bit_exact(dev, bits, dbits, I, K, norm
     gam = S.norm_weight(K, g).to(dev)
     eps = 1e-6
     y16 = torch.empty(I, dtype=torch.float16, device=dev)
+    ys = torch.full((I,), float("nan"), dtype=torch.float16, device=dev)
     h = torch.full((I,), float("nan"), dtype=torch.float32, device=dev)
     gu = torch.empty(2 * I, dtype=torch.float16, device=dev)
     d1 = torch.empty(N, dtype=torch.float16, device=dev)
@@ -216,23 +226,41 @@ def test_gate_up_silu_pair_then_fwht_gemv_bit_exact(dev, bits, dbits, I, K, norm
         R.call("r4q_gate_up_silu_fwht", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
                res1.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), y16.data_ptr(), I, K, bits, st)
         R.call("r4q_gate_up_silu", a.data_ptr(), b.data_ptr(), gam.data_ptr(), res2.data_ptr(),
-               eps, w.data_ptr(), sz.data_ptr(), h.data_ptr(), I, K, bits, st)
+               eps, w.data_ptr(), sz.data_ptr(), ys.data_ptr(), h.data_ptr(), split, I, K, bits,
+               st)
         R.call("r4q_res_rmsnorm_fwht_gemv", a.data_ptr(), b.data_ptr(), gam.data_ptr(),
                res1.data_ptr(), eps, w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K, bits, st)
     else:
         R.call("r4q_gate_up_silu_fwht", a.data_ptr(), None, None, None, eps, w.data_ptr(),
                sz.data_ptr(), y16.data_ptr(), I, K, bits, st)
         R.call("r4q_gate_up_silu", a.data_ptr(), None, None, None, eps, w.data_ptr(),
-               sz.data_ptr(), h.data_ptr(), I, K, bits, st)
+               sz.data_ptr(), ys.data_ptr(), h.data_ptr(), split, I, K, bits, st)
         R.call("r4q_gemv", a.data_ptr(), w.data_ptr(), sz.data_ptr(), gu.data_ptr(), 2 * I, K,
                bits, st)
     R.call("r4q_gemv", y16.data_ptr(), wd.data_ptr(), szp, d1.data_ptr(), N, I, dbits, st)
-    R.call("r4q_fwht_gemv", h.data_ptr(), wd.data_ptr(), szp, d2.data_ptr(), N, I, dbits, st)
+    R.call("r4q_fwht_gemv", ys.data_ptr(), h.data_ptr(), split, wd.data_ptr(), szp,
+           d2.data_ptr(), N, I, dbits, st)
     torch.cuda.synchronize()
-    assert torch.isfinite(h).all()
+    assert torch.equal(ys[:split].view(torch.int16), y16[:split].view(torch.int16))
+    assert torch.isfinite(h[split:]).all()
     assert torch.equal(d1.view(torch.int16), d2.view(torch.int16))
     if norm:
         assert torch.equal(res1.view(torch.int16), res2.view(torch.int16))
-    # the oracle rounds the product to fp16 (and its exp is numpy's)
-    want = O.silu_mul(gu[:I].cpu().numpy(), gu[I:].cpu().numpy())
-    assert rel_l2(h.cpu().numpy(), want) <= 1e-3
+    if split < I:
+        # the oracle rounds the product to fp16 (and its exp is numpy's)
+        want = O.silu_mul(gu[split:I].cpu().numpy(), gu[I + split:].cpu().numpy())
+        assert rel_l2(h[split:].cpu().numpy(), want) <= 1e-3
+
+
+def test_gate_up_silu_split_rejects_bad_split(dev):
+    import r4q_lib as R
+    I, K = 64, 256
+    w = torch.zeros(2 * I, K // 2, dtype=torch.uint8, device=dev)
+    sz = torch.zeros(2 * I, K // 32, dtype=torch.int32, device=dev)
+    a = torch.zeros(K, dtype=torch.float16, device=dev)
+    y = torch.empty(I, dtype=torch.float16, device=dev)
+    h = torch.empty(I, dtype=torch.float32, device=dev)
+    for split in (-32, 16, I + 32):
+        with pytest.raises(RuntimeError):
+            R.call("r4q_gate_up_silu", a.data_ptr(), None, None, None, 1e-6, w.data_ptr(),
+                   sz.data_ptr(), y.data_ptr(), h.data_ptr(), split, I, K, 4, R.stream_handle())
