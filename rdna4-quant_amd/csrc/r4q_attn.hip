@@ -121,9 +121,12 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   // end are clamped to its last row and masked.
   auto vpos = [&](int s) { return s < 4 ? 4 * g + s : 16 + 4 * g + (s - 4); };
   // One register set per wave: the next chunk's K (V) loads are issued as
-  // soon as this chunk's K (V) registers are converted (a second set in
-  // flight measured no faster: 19.5 vs 19.6 us at 32K positions, slower at
-  // 2K-8K).  Byte offsets are 32-bit from the workgroup's uniform row base.
+  // soon as this chunk's K (V) registers are converted.  They are issued
+  // unconditionally (past the wave's last chunk they read the clamped last
+  // row again): loads issued on only some paths make the compiler wait for
+  // every load in flight before the next use of the set, which would stall
+  // each chunk on its successor's loads.  Byte offsets are 32-bit from the
+  // workgroup's uniform row base.
   u4_t kr0[2][2];
   u2_t vr0[8];
   auto load_k = [&](u4_t (&kr)[2][2], int c) {
@@ -250,7 +253,6 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   // one chunk from the register set (kr, vr), which then receives this
   // wave's next chunk (c + 4)
   auto step = [&](u4_t (&kr)[2][2], u2_t (&vr)[8], int c) {
-    const bool more = c + 4 < nchunk;  // wave-uniform
     // ---- K -> fp16 A operands, S^T = K Q^T, then the set's next K in flight
     f4_t sacc[2];
 #pragma unroll
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) sacc[bb] = mfma16(ka[j], qb[j], sacc[bb]);
     }
-    if (more) load_k(kr, c + 4);
+    load_k(kr, c + 4);
 
     // ---- online softmax for head col over positions 32c + vpos(s)
     float sv[8];
@@ -332,7 +334,14 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
       transpose4x4(vhi + 4, x);
       for (int d = 0; d < 4; ++d) tr[4 + d][1] = x[d];
     }
-    if (more) load_v(vr, c + 4);
+    // the transposes above are the set's last reads: the empty asm (inputs:
+    // every transposed word; memory clobber) keeps them before the next
+    // chunk's loads, so that the loads refill the same registers (a load
+    // hoisted above them needs other registers and a copy back at the loop
+    // end, which waits for it)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) asm volatile("" : "+v"(tr[d][0]), "+v"(tr[d][1])::"memory");
+    load_v(vr, c + 4);
     if (rescale) {
       float ar[4];  // alpha of the C rows' heads 4g + r (lane 4g + r holds that head)
 #pragma unroll
@@ -349,7 +358,13 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
       o[d] = mfma16(pa, vb, o[d]);
     }
   };
-  for (int c = wave; c < nchunk; c += 4) step(kr0, vr0, c);
+  // The first chunk is peeled: every path into the loop then comes from a
+  // step, which issues the next K before the next V, so the loop's first K
+  // wait leaves the V loads in flight (the prologue's order may differ).
+  if (wave < nchunk) {
+    step(kr0, vr0, wave);
+    for (int c = wave + 4; c < nchunk; c += 4) step(kr0, vr0, c);
+  }
 
   // ---- merge the 4 waves (each: max and sum per head, O rows per head)
   float lsum = l_run + __shfl_xor(l_run, 16);
