@@ -108,7 +108,9 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   __shared__ __align__(16) float ostage[G][128];
   __shared__ float fin[G][2];  // merged max, sum
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  // wave index as a scalar: the chunk loops and the per-chunk guards are
+  // then scalar branches (an MFMA computes its whole tile whatever EXEC holds)
+  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int col = lane & 15, g = lane >> 4;
   const float ks = ksc ? ksc[kh] : 1.0f;
   const float vs = vsc ? vsc[kh] : 1.0f;
@@ -250,9 +252,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  // one chunk from the register set (kr, vr), which then receives this
-  // wave's next chunk (c + 4)
-  auto step = [&](u4_t (&kr)[2][2], u2_t (&vr)[8], int c) {
+  // one chunk c from the register set (kr, vr), which then receives chunk
+  // cn.  A chunk past the split's last one (c >= nchunk) starts at or after
+  // position L, so every score is masked to -inf: it adds nothing (p = 0,
+  // alpha = 1 once a real chunk has set the running max)
+  auto step = [&](u4_t (&kr)[2][2], u2_t (&vr)[8], int c, int cn) {
     // ---- K -> fp16 A operands, S^T = K Q^T, then the set's next K in flight
     f4_t sacc[2];
 #pragma unroll
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) sacc[bb] = mfma16(ka[j], qb[j], sacc[bb]);
     }
-    load_k(kr, c + 4);
+    load_k(kr, cn);
 
     // ---- online softmax for head col over positions 32c + vpos(s)
     float sv[8];
@@ -341,7 +345,7 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // end, which waits for it)
 #pragma unroll
     for (int d = 0; d < 8; ++d) asm volatile("" : "+v"(tr[d][0]), "+v"(tr[d][1])::"memory");
-    load_v(vr, c + 4);
+    load_v(vr, cn);
     if (rescale) {
       float ar[4];  // alpha of the C rows' heads 4g + r (lane 4g + r holds that head)
 #pragma unroll
@@ -361,9 +365,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   // The first chunk is peeled: every path into the loop then comes from a
   // step, which issues the next K before the next V, so the loop's first K
   // wait leaves the V loads in flight (the prologue's order may differ).
+  // (A second register set, chunk c + 8 in flight while c and c + 4 are
+  // computed, measured no faster at 32K positions and slower at 8K.)
   if (wave < nchunk) {
-    step(kr0, vr0, wave);
-    for (int c = wave + 4; c < nchunk; c += 4) step(kr0, vr0, c);
+    step(kr0, vr0, wave, wave + 4);
+    for (int c = wave + 4; c < nchunk; c += 4) step(kr0, vr0, c, c + 4);
   }
 
   // ---- merge the 4 waves (each: max and sum per head, O rows per head)

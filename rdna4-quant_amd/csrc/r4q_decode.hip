@@ -55,6 +55,8 @@ struct Dims {
 
 struct Bufs {
   uint16_t *h, *r, *rot, *qkv, *o, *gu, *y, *d, *logits;
+  void* ws = nullptr;  // split-K partials of the batched projections
+  size_t ws_bytes = 0;
   float* attn;
   int* state;
   int64_t* ids;
@@ -111,13 +113,31 @@ int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsp
                           B * I, B * D, B * lmN};
   size_t total = 0;
   for (size_t s : sizes) total += align256(s * 2);
-  R4Q_TRY(ctx->step.reserve(total));
+  // workspace of the batched projections (split-K partials): the largest
+  // any of the step's matrices asks for
+  size_t gws = 0;
+  if (B > 1) {
+    auto need = [&](int64_t N, int64_t K, int bits) {
+      gws = std::max(gws, gemm_ws_need(B, N, K, bits));
+    };
+    for (int li = 0; li < dm.L; ++li) {
+      const r4q_layer& y = m->layers[li];
+      need(dm.qkvN, dm.D, y.qkv_bits);
+      need(dm.D, dm.qd, y.o_bits);
+      need(2 * (int64_t)dm.I, dm.D, y.gu_bits);
+      need(dm.D, dm.I, y.down_bits);
+    }
+    if (m->final_norm) need(m->lm_N, m->lm_K, m->lm_bits);
+  }
+  R4Q_TRY(ctx->step.reserve(total + gws));
   uint16_t** dst[] = {&bf.h, &bf.r, &bf.rot, &bf.qkv, &bf.o, &bf.gu, &bf.y, &bf.d, &bf.logits};
   uint8_t* p = static_cast<uint8_t*>(ctx->step.ptr);
   for (int i = 0; i < 9; ++i) {
     *dst[i] = reinterpret_cast<uint16_t*>(p);
     p += align256(sizes[i] * 2);
   }
+  bf.ws = gws ? p : nullptr;
+  bf.ws_bytes = gws;
   R4Q_TRY(ctx->attn.reserve(attn_ws_bytes(B, dm.H, nsplit)));
   bf.attn = static_cast<float*>(ctx->attn.ptr);
   const size_t misc = align256(kStateWords * 4) + align256(B * 8) +
@@ -131,9 +151,9 @@ int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsp
 }
 
 int linear(const void* x, const void* w, const void* s, void* y, int64_t B, int64_t N, int64_t K,
-           int bits, hipStream_t st) {
+           int bits, hipStream_t st, const Bufs& bf) {
   if (B == 1) return gemv_launch(x, w, s, y, N, K, bits, st);
-  return gemm_launch(x, w, s, y, B, N, K, bits, st);
+  return gemm_launch(x, w, s, y, B, N, K, bits, st, bf.ws, bf.ws_bytes);
 }
 
 // Optional event recorder for the per-category profile.
@@ -175,7 +195,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     const r4q_layer& y = m->layers[li];
     prof.mark(st, kGemv);
     if (!fused) {
-      R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st));
+      R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st, bf));
     } else if (li == 0) {  // input hidden state: plain RMSNorm
       R4Q_TRY(gemv_norm_launch(bf.h, nullptr, y.in_norm, nullptr, eps, y.qkv_w, y.qkv_s, bf.qkv,
                                dm.qkvN, D, y.qkv_bits, st));
@@ -194,7 +214,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
                                 bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
                                 nsplit, 1, bf.attn, st, &qk));
     prof.mark(st, kGemv);
-    R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st));
+    R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st, bf));
     // gate/up: r = fp16(o + h), RMSNorm + FWHT in the staging and, for
     // INT4/INT8, the SiLU-gate in the epilogue: fp16 FWHT'd output for the
     // whole 64-row units below the split (a multiple of the CU count, one
@@ -219,12 +239,12 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
         prof.mark(st, kNorm);
         R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
         prof.mark(st, kGemv);
-        R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st));
+        R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st, bf));
       }
       prof.mark(st, kNorm);
       R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
       prof.mark(st, kGemv);
-      R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st));
+      R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st, bf));
     }
     if (!fused) {
       prof.mark(st, kNorm);
@@ -243,7 +263,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     R4Q_TRY(launch_rownorm(3, bf.d, bf.r, m->layers[0].in_norm, bf.rot, bf.h, B, D, eps, st));
   } else if (logits) {
     prof.mark(st, kGemv);
-    R4Q_TRY(linear(bf.rot, m->lm_w, m->lm_s, bf.logits, B, m->lm_N, m->lm_K, m->lm_bits, st));
+    R4Q_TRY(linear(bf.rot, m->lm_w, m->lm_s, bf.logits, B, m->lm_N, m->lm_K, m->lm_bits, st, bf));
   }
   prof.mark(st, kEnd);
   return R4Q_OK;
@@ -591,11 +611,11 @@ extern "C" int r4q_prefill_logits(r4q_ctx* ctx, const r4q_model* m, const void* 
   size_t gws = 0;
   for (int li = 0; li < dm.L; ++li) {
     const r4q_layer& ly = m->layers[li];
-    gws = std::max({gws, gemm_ws_bytes(M, dm.qkvN, D, ly.qkv_bits),
-                    gemm_ws_bytes(M, D, dm.qd, ly.o_bits), gemm_ws_bytes(M, 2 * I, D, ly.gu_bits),
-                    gemm_ws_bytes(M, D, I, ly.down_bits)});
+    gws = std::max({gws, gemm_ws_need(M, dm.qkvN, D, ly.qkv_bits),
+                    gemm_ws_need(M, D, dm.qd, ly.o_bits), gemm_ws_need(M, 2 * I, D, ly.gu_bits),
+                    gemm_ws_need(M, D, I, ly.down_bits)});
   }
-  if (logits) gws = std::max(gws, gemm_ws_bytes(M, m->lm_N, m->lm_K, m->lm_bits));
+  if (logits) gws = std::max(gws, gemm_ws_need(M, m->lm_N, m->lm_K, m->lm_bits));
   R4Q_TRY(ctx->prefill.reserve(total + gws));
   uint16_t* buf[8];
   uint8_t* p = static_cast<uint8_t*>(ctx->prefill.ptr);

@@ -14,10 +14,14 @@
 //    deterministic split-K over a caller workspace (see its comment);
 //  * gemm_mfma_kernel (17 <= M < 256, and FP16 weights): 128 x 128 tiles,
 //    X and the dequantised W staged in LDS per 32-wide K step;
-//  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows.
+//  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows
+//    through an LDS ring (split along K for narrow N).
 // Dequantised values equal r4q_dequant_int4/8 bit-for-bit
 // (fp16((q - zp) * scale) from an exact product, one rounding).
+#include <stdint.h>
 #include <stdlib.h>
+
+#include <algorithm>
 
 #include "r4q_device.hpp"
 #include "r4q_gemv.hpp"
@@ -172,45 +176,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------------
-// Skinny GEMM for 2..16 activation rows (batched decode): the weights are
-// streamed once for all rows.  v_mfma_f32_16x16x32_f16 with A = the x rows
-// (padded to 16 by repeating the last row) and B = dequantised weights.
-//
-// One iteration of a wave: every lane loads one 16-byte chunk of a weight
-// row (lane l: row n0 + l%16, chunk group g = l/16), so the 4 lane groups
-// hold 4 consecutive chunks of each of 16 rows (64 contiguous bytes per row).
-// The MFMA contraction index k is only a label: lane group g's 8 k-slots of
-// MFMA d carry elements of chunk g, and the A fragment of that lane group
-// holds the x values of exactly those elements.  Because the weights are
-// fully dequantised before the MFMA -- fp16((q - zp) * s) by an exact packed
-// fp16 subtraction and one rounded packed multiply, bit-identical to the
-// dequant kernel -- the accumulation may run across blocks.
-//   INT4: chunk = one 32-element block, 4 MFMAs per iteration; nibble pairs
-//         (q_p, q_p+4) come from (w >> 4p) & 0x000F000F | 0x64006400, so x is
-//         permuted to (x_p, x_p+4) pairs;
-//   INT8: chunk = half a block, 2 MFMAs; byte pairs by v_perm, natural order;
-//   FP16: chunk = 8 weights, 1 MFMA.
-// A workgroup (4 waves) owns 16*T weight rows; wave w takes iterations
-// w, w+4, ...; the 4 partial tiles meet in LDS.
-template <int WBITS>
-struct Skinny;
-template <>
-struct Skinny<4> {
-  static constexpr int kKPI = 128;  // k per iteration (4 lane groups)
-  static constexpr int kMfma = 4;
-};
-template <>
-struct Skinny<8> {
-  static constexpr int kKPI = 64;
-  static constexpr int kMfma = 2;
-};
-template <>
-struct Skinny<16> {
-  static constexpr int kKPI = 32;
-  static constexpr int kMfma = 1;
-};
-
-// B fragment of MFMA d from the lane's 16-byte chunk.
+// Weight fragments of the skinny GEMM (below).  The MFMA contraction index k
+// is only a label: lane group g's 8 k-slots of an MFMA carry 8 weight
+// elements, and the A fragment of that lane group holds the activation
+// values of exactly those elements.  Because the weights are fully
+// dequantised before the MFMA -- fp16((q - zp) * s) by an exact packed fp16
+// subtraction and one rounded packed multiply, bit-identical to the dequant
+// kernel -- the accumulation may run across blocks.
+//   INT4: 4 MFMAs per 16 weight bytes; nibble pairs (q_p, q_p+4) come from
+//         (w >> 4p) & 0x000F000F | 0x64006400, so the activation is permuted
+//         to (x_p, x_p+4) pairs;
+//   INT8: 2 MFMAs per 16 bytes; byte pairs by v_perm, natural order;
+//   FP16: 1 MFMA per 16 bytes.
+// B fragment of MFMA d from 16 weight bytes w and the block's (scale, zero) s2.
 template <int WBITS>
 __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
   if constexpr (WBITS == 16) {
@@ -237,117 +215,6 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) o[p] = as_u32((as_h2(pr[p]) + nz) * sc);
     return __builtin_bit_cast(h8_t, o);
-  }
-}
-
-// A fragment of MFMA d: the 8 x values whose labels match skinny_b's slots.
-template <int WBITS>
-__device__ __forceinline__ h8_t skinny_a(const uint16_t* __restrict__ xrow, int kchunk, int d) {
-  if constexpr (WBITS == 4) {
-    const u4_t v = *reinterpret_cast<const u4_t*>(xrow + kchunk + 8 * d);
-    // (x0 x1) (x2 x3) (x4 x5) (x6 x7) -> (x0 x4) (x1 x5) (x2 x6) (x3 x7)
-    u4_t o;
-    o[0] = (v[0] & 0xFFFFu) | (v[2] << 16);
-    o[1] = (v[0] >> 16) | (v[2] & 0xFFFF0000u);
-    o[2] = (v[1] & 0xFFFFu) | (v[3] << 16);
-    o[3] = (v[1] >> 16) | (v[3] & 0xFFFF0000u);
-    return __builtin_bit_cast(h8_t, o);
-  } else {
-    return __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(xrow + kchunk + 8 * d));
-  }
-}
-
-template <int WBITS, int T, int U, bool ROLL>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
-                                                          const uint8_t* __restrict__ W,
-                                                          const uint32_t* __restrict__ SZ,
-                                                          uint16_t* __restrict__ Y, int M, int N,
-                                                          int K) {
-  constexpr int KPI = Skinny<WBITS>::kKPI;
-  constexpr int NM = Skinny<WBITS>::kMfma;
-  constexpr int CK = KPI / 4;  // elements per lane chunk
-  __shared__ __align__(16) float red[4][T][64][4];
-  // The wave index is made a scalar so that the K loop and the per-batch
-  // guards below are scalar branches: an MFMA computes its whole tile
-  // whatever EXEC holds, so a guard lowered to an EXEC mask would not skip it.
-  const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int g = lane >> 4, r16 = lane & 15;
-  const int n0 = blockIdx.x * 16 * T;
-  const int iters = K / KPI;
-  const int64_t row_bytes = (int64_t)K * WBITS / 8;
-  const int nb = K / 32;
-  const uint16_t* xrow = X + (int64_t)min(r16, M - 1) * K;  // A row of this lane
-
-  f4_t acc[T];
-#pragma unroll
-  for (int i = 0; i < T; ++i) acc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-  // Batches of U iterations (iterations past the end load the last one
-  // again and are not computed).  ROLL: two register sets, the next batch's
-  // loads issued before the current batch is multiplied, so a batch is
-  // always in flight -- faster when the grid has few workgroups (N <= 7168:
-  // 10-20%), slower when it has many (gate_up: 57 -> 62 us at batch 8).
-  struct Batch {
-    u4_t wv[U][T];
-    uint32_t s2[U][T];
-    h8_t a[U][NM];
-  };
-  auto load = [&](Batch& bt, int it0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int it = min(it0 + 4 * u, iters - 1);
-      const int kchunk = it * KPI + g * CK;  // first element of this lane's chunk
-#pragma unroll
-      for (int i = 0; i < T; ++i) {
-        const int64_t n = min(n0 + 16 * i + r16, N - 1);  // clamped: in bounds
-        bt.wv[u][i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u4_t*>(W + n * row_bytes + (int64_t)kchunk * WBITS / 8));
-        bt.s2[u][i] = (WBITS == 16) ? 0u : SZ[n * nb + kchunk / 32];
-      }
-#pragma unroll
-      for (int d = 0; d < NM; ++d) bt.a[u][d] = skinny_a<WBITS>(xrow, kchunk, d);
-    }
-  };
-  auto compute = [&](const Batch& bt, int it0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (it0 + 4 * u < iters) {  // wave-uniform
-#pragma unroll
-        for (int i = 0; i < T; ++i)
-#pragma unroll
-          for (int d = 0; d < NM; ++d)
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                bt.a[u][d], skinny_b<WBITS>(bt.wv[u][i], bt.s2[u][i], d), acc[i], 0, 0, 0);
-      }
-    }
-  };
-  if constexpr (ROLL) {
-    Batch b0, b1;
-    load(b0, wave);
-    for (int it0 = wave; it0 < iters; it0 += 8 * U) {
-      load(b1, it0 + 4 * U);
-      compute(b0, it0);
-      load(b0, it0 + 8 * U);
-      compute(b1, it0 + 4 * U);
-    }
-  } else {
-    for (int it0 = wave; it0 < iters; it0 += 4 * U) {
-      Batch b0;
-      load(b0, it0);
-      compute(b0, it0);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < T; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][i][lane][r] = acc[i][r];
-  __syncthreads();
-  // C fragment: lane holds rows m = 4*(lane/16) + r, column n = lane % 16
-  for (int e = t; e < T * 64 * 4; e += 256) {
-    const int i = e / 256, l = (e / 4) & 63, r = e & 3;
-    const int m = 4 * (l >> 4) + r, n = n0 + 16 * i + (l & 15);
-    const float v = (red[0][i][l][r] + red[1][i][l][r]) + (red[2][i][l][r] + red[3][i][l][r]);
-    if (m < M && n < N) Y[(int64_t)m * N + n] = f2h(v);
   }
 }
 
@@ -617,44 +484,254 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   Y[(int64_t)row * N + col] = f2h(v);
 }
 
+// ---------------------------------------------------------------------
+// Skinny GEMM for 2 <= M <= 16 rows (batched decode) through an LDS ring.
+// A workgroup (4 waves) owns 64 weight rows (16 per wave) and a range of K
+// steps; each step stages, by global->LDS copies, 128 bytes of every weight
+// row (8 rows x 128 B per copy instruction: whole cache lines, which reads
+// the weights at ~5.6-6 TB/s where 16 rows x 64 B per instruction -- the
+// MFMA B-fragment layout loaded straight into registers -- measured
+// 4.4-4.9 TB/s), the rows' (scale, zero) words and the matching slice of the
+// MR activation rows.  kSkStages steps are in flight; one barrier per step
+// (the ring of gemm_ring_kernel).  Per step each wave runs KS/32 MFMA
+// 16x16x32 tiles: B = its 16 weight rows dequantised from LDS (skinny_b),
+// A = the activation rows (skinny_a's element order), C = 16 activation
+// rows x 16 weight rows.  Lane group g of MFMA j holds the k labels
+// k0 + (KS/4) g + 8 j .. +7 in both operands, so each lane reads its 32
+// weight bytes of the step with two 16-byte LDS reads.  The 16-byte pieces
+// of a row sit in LDS slot piece ^ (row & 7) (bank spread).
+// Split-K (S > 1): the workgroup covers steps [s kps, (s+1) kps) and writes
+// fp32 partials part[s][m][n]; gemm_skinny_reduce_kernel sums them in order.
+constexpr int kSkTile = 64;   // weight rows per workgroup
+constexpr int kSkStages = 3;  // steps in flight
+constexpr int kSkMaxSplits = 8;
+
+template <int WBITS, int MR>
+struct SkRing {
+  static constexpr int kKS = 1024 / WBITS;          // k per step: 128 B of each weight row
+  static constexpr int kSteps = kKS / 32;           // MFMA k-steps per step
+  static constexpr int kW = kSkTile * 128;          // weights: 8 KB
+  static constexpr int kSRow = WBITS == 16 ? 0 : (kKS / 32) * 4;  // (scale, zero) bytes per row
+  static constexpr int kS = kSkTile * kSRow;        // 2 KB (INT4) / 1 KB (INT8) / 0
+  static constexpr int kXRow = kKS * 2;             // activation bytes per row per step
+  static constexpr int kX = MR * kXRow;
+  static constexpr int kStage = kW + kS + kX;
+  static constexpr bool kX16 = kX >= 4096;          // activation as 1 KB copies (else 256 B)
+  static constexpr int kCX = kX16 ? kX / 4096 : kX / 1024;  // activation copies per wave
+  static constexpr int kCS = WBITS == 4 ? 2 : WBITS == 8 ? 1 : 0;  // scale copies (256 B) per wave
+  static constexpr int kPer = 2 + kCS + kCX;        // copies per wave per step
+  static_assert(kX % (kX16 ? 4096 : 1024) == 0 && kCX >= 1, "activation copies must split evenly");
+};
+
+// Copies step kb of the workgroup's weight rows, scales and activation rows
+// into ring stage `stage` (rows past N / M clamped to the last one).
+template <int WBITS, int MR>
+__device__ __forceinline__ void sk_issue(uint8_t* stage, const uint16_t* __restrict__ X,
+                                         const uint8_t* __restrict__ W,
+                                         const uint32_t* __restrict__ SZ, int M, int N, int K,
+                                         int n0, int kb, int wave, int lane) {
+  using R = SkRing<WBITS, MR>;
+  const int64_t row_bytes = (int64_t)K * WBITS / 8;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // weights: copy c covers tile rows 8c .. 8c+7
+    const int c = 2 * wave + i, r = 8 * c + (lane >> 3);
+    const int piece = (lane & 7) ^ (r & 7);
+    const int64_t n = min(n0 + r, N - 1);
+    copy16(W + n * row_bytes + (int64_t)kb * 128 + 16 * piece, stage + 1024 * c);
+  }
+  if constexpr (WBITS != 16) {
+    const int nb = K / 32;
+    constexpr int wpr = R::kSRow / 4;   // scale words per row per step
+    constexpr int rpc = 64 / wpr;       // rows per 256-byte copy
+#pragma unroll
+    for (int i = 0; i < R::kCS; ++i) {
+      const int c = R::kCS * wave + i, r = rpc * c + lane / wpr;
+      const int64_t n = min(n0 + r, N - 1);
+      copy4(SZ + n * nb + (int64_t)kb * wpr + lane % wpr, stage + R::kW + 256 * c);
+    }
+  }
+  const uint16_t* xs = X + (int64_t)kb * R::kKS;
+#pragma unroll
+  for (int i = 0; i < R::kCX; ++i) {
+    const int c = R::kCX * wave + i;
+    if constexpr (R::kX16) {  // 1 KB per copy, 16 bytes per lane
+      const int off = 1024 * c + 16 * lane;
+      const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
+      const int64_t m = min(r, M - 1);
+      copy16(xs + m * K + 8 * (slot ^ (r & 7)), stage + R::kW + R::kS + 1024 * c);
+    } else {  // 256 B per copy, 4 bytes per lane
+      const int off = 256 * c + 4 * lane;
+      const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
+      const int64_t m = min(r, M - 1);
+      copy4(xs + m * K + 8 * (slot ^ (r & 7)) + 2 * (lane & 3),
+            stage + R::kW + R::kS + 256 * c);
+    }
+  }
+}
+
+template <int WBITS, int MR>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
+                                                          const uint8_t* __restrict__ W,
+                                                          const uint32_t* __restrict__ SZ,
+                                                          uint16_t* __restrict__ Y,
+                                                          float* __restrict__ part, int M, int N,
+                                                          int K, int ntiles, int kps) {
+  using R = SkRing<WBITS, MR>;
+  constexpr int D = kSkStages;
+  __shared__ __align__(16) uint8_t ring[D * R::kStage];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
+  const int n0 = tile * kSkTile;
+  const int kt = K / R::kKS;
+  const int kb0 = sp * kps, nk = min(kt - kb0, kps);  // >= 1 (host)
+  const int col = lane & 15, g = lane >> 4;
+  const int wrow = 16 * wave + col;                   // this lane's weight row in the tile
+  const int xr = col % MR;                            // activation row (rows >= MR: duplicates)
+
+  f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s)
+    sk_issue<WBITS, MR>(ring + s * R::kStage, X, W, SZ, M, N, K, n0, kb0 + min(s, nk - 1), wave,
+                        lane);
+  for (int i = 0; i < nk; ++i) {
+    wait_copies<(D - 2) * R::kPer>();  // this wave's copies of step i have landed
+    ring_barrier();                    // every wave's; every wave is done with step i-1
+    sk_issue<WBITS, MR>(ring + ((i + D - 1) % D) * R::kStage, X, W, SZ, M, N, K, n0,
+                        kb0 + min(i + D - 1, nk - 1), wave, lane);
+    const uint8_t* st = ring + (i % D) * R::kStage;
+    // weight bytes [32 g, 32 g + 32) of row wrow: pieces 2g, 2g+1
+    const u4_t b0 = *reinterpret_cast<const u4_t*>(st + 128 * wrow + 16 * ((2 * g) ^ (wrow & 7)));
+    const u4_t b1 =
+        *reinterpret_cast<const u4_t*>(st + 128 * wrow + 16 * ((2 * g + 1) ^ (wrow & 7)));
+    uint32_t sw0 = 0u, sw1 = 0u;
+    if constexpr (WBITS == 4) {  // blocks 2g, 2g+1 of the step
+      const uint2 v = *reinterpret_cast<const uint2*>(st + R::kW + R::kSRow * wrow + 8 * g);
+      sw0 = v.x;
+      sw1 = v.y;
+    } else if constexpr (WBITS == 8) {  // block g
+      sw0 = *reinterpret_cast<const uint32_t*>(st + R::kW + R::kSRow * wrow + 4 * g);
+    }
+    const uint8_t* xst = st + R::kW + R::kS + R::kXRow * xr;
+#pragma unroll
+    for (int j = 0; j < R::kSteps; ++j) {
+      // activation piece holding k labels k0 + (KS/4) g + 8 j .. +7
+      const int piece = (R::kKS / 32) * g + j;
+      const u4_t av = *reinterpret_cast<const u4_t*>(xst + 16 * (piece ^ (xr & 7)));
+      h8_t a;
+      if constexpr (WBITS == 4) {  // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
+        u4_t o;
+        o[0] = (av[0] & 0xFFFFu) | (av[2] << 16);
+        o[1] = (av[0] >> 16) | (av[2] & 0xFFFF0000u);
+        o[2] = (av[1] & 0xFFFFu) | (av[3] << 16);
+        o[3] = (av[1] >> 16) | (av[3] & 0xFFFF0000u);
+        a = __builtin_bit_cast(h8_t, o);
+      } else {
+        a = __builtin_bit_cast(h8_t, av);
+      }
+      h8_t b;
+      if constexpr (WBITS == 4) b = skinny_b<4>(j < 4 ? b0 : b1, j < 4 ? sw0 : sw1, j & 3);
+      else if constexpr (WBITS == 8) b = skinny_b<8>(j < 2 ? b0 : b1, sw0, j & 1);
+      else b = __builtin_bit_cast(h8_t, j == 0 ? b0 : b1);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+  wait_copies<0>();  // no copy into LDS outlives the workgroup
+  // C: lane holds activation rows 4g + r, weight row n0 + 16 wave + col
+  const int n = n0 + 16 * wave + col;
+  if (n < N) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * g + r;
+      if (m < M) {
+        if (part) part[((int64_t)sp * M + m) * N + n] = acc[r];
+        else Y[(int64_t)m * N + n] = f2h(acc[r]);
+      }
+    }
+  }
+}
+
+// Y[m][n] = fp16(sum over s of part[s][m][n]), in split order.
+__global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(const float* __restrict__ part,
+                                                                 uint16_t* __restrict__ Y, int M,
+                                                                 int N, int S) {
+  const int n = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+  if (n >= N) return;
+  const int64_t plane = (int64_t)M * N;
+  const float* p = part + (int64_t)m * N + n;
+  float v = p[0];
+  for (int z = 1; z < S; ++z) v += p[z * plane];
+  Y[(int64_t)m * N + n] = f2h(v);
+}
+
 }  // namespace
 
 bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
-  const int kpi = wbits == 4 ? Skinny<4>::kKPI : wbits == 8 ? Skinny<8>::kKPI : Skinny<16>::kKPI;
-  return M >= 2 && M <= 16 && K % kpi == 0;
+  const int64_t ks = 1024 / (wbits == 4 ? 4 : wbits == 8 ? 8 : 16);  // k per ring step
+  return M >= 2 && M <= 16 && K % ks == 0;
+}
+
+// Split count of the skinny ring: toward ~512 workgroups when the 64-row
+// tiles alone are fewer, each split keeping at least 8 K steps (measured at
+// M = 8: down 5120 x 17408 7 splits 23.6 us, 4: 26.1, none: 53.4; qkv
+// 7168 x 5120 2 splits 12.8 us, 5: 14.8, none: 17.5); S > 1 needs
+// S * M * N fp32 of workspace.
+int skinny_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  const int64_t ntiles = (N + kSkTile - 1) / kSkTile;
+  const int64_t kt = K / (1024 / wbits);
+  int64_t S = (512 + ntiles - 1) / ntiles;
+  S = std::min<int64_t>(S, std::min<int64_t>(kSkMaxSplits, kt / 8));
+  if (const char* e = getenv("R4Q_SKINNY_SPLITS")) S = atoi(e);  // tuning override
+  if (S < 2) return 1;
+  // every split non-empty
+  const int64_t kps = (kt + S - 1) / S;
+  S = (kt + kps - 1) / kps;
+  if ((size_t)S * M * N * 4 > ws_bytes) return 1;
+  return (int)S;
+}
+
+size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
+  const int S = skinny_splits(M, N, K, wbits, SIZE_MAX);
+  return S > 1 ? (size_t)S * M * N * 4 : 0;
 }
 
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
-                       int64_t N, int64_t K, int wbits, hipStream_t st) {
-  constexpr int T = 2;
-  const int64_t wgs = (N + 16 * T - 1) / (16 * T);
-  const dim3 grid((unsigned)wgs);
+                       int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
+                       size_t ws_bytes) {
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
-  // rolling two-set batches of 2 for small grids, single batches of 4 for
-  // grids that fill the chip several times over (measured at batch 8)
-  const bool roll = wgs < 512;
-#define R4Q_SKINNY(WB)                                                                        \
-  if (roll)                                                                                   \
-    hipLaunchKernelGGL((gemm_skinny_kernel<WB, T, 2, true>), grid, dim3(256), 0, st, xp, wp,   \
-                       sp, yp, (int)M, (int)N, (int)K);                                       \
-  else                                                                                        \
-    hipLaunchKernelGGL((gemm_skinny_kernel<WB, T, 4, false>), grid, dim3(256), 0, st, xp, wp,  \
-                       sp, yp, (int)M, (int)N, (int)K);
+  const int S = skinny_splits(M, N, K, wbits, ws ? ws_bytes : 0);
+  const int64_t ntiles = (N + kSkTile - 1) / kSkTile;
+  const int64_t kt = K / (1024 / wbits);
+  const int kps = (int)((kt + S - 1) / S);
+  float* part = S > 1 ? static_cast<float*>(ws) : nullptr;
+  const dim3 grid((unsigned)(ntiles * S));
+#define R4Q_SKINNY(WB, MRR)                                                                    \
+  hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR>), grid, dim3(256), 0, st, xp, wp, sp, yp,    \
+                     part, (int)M, (int)N, (int)K, (int)ntiles, kps)
+  const bool m8 = M <= 8;
   switch (wbits) {
     case 4:
-      R4Q_SKINNY(4)
+      if (m8) R4Q_SKINNY(4, 8);
+      else R4Q_SKINNY(4, 16);
       break;
     case 8:
-      R4Q_SKINNY(8)
+      if (m8) R4Q_SKINNY(8, 8);
+      else R4Q_SKINNY(8, 16);
       break;
     default:
-      R4Q_SKINNY(16)
+      if (m8) R4Q_SKINNY(16, 8);
+      else R4Q_SKINNY(16, 16);
   }
 #undef R4Q_SKINNY
-  return launch_status("gemm_skinny");
+  R4Q_TRY(launch_status("gemm_skinny"));
+  if (S > 1) {
+    hipLaunchKernelGGL(gemm_skinny_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M),
+                       dim3(256), 0, st, part, yp, (int)M, (int)N, S);
+    R4Q_TRY(launch_status("gemm_skinny_reduce"));
+  }
+  return R4Q_OK;
 }
 
 bool gemm_ring_ok(int64_t M, int wbits) { return M >= RBM && wbits != 16; }

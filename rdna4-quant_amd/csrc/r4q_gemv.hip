@@ -769,10 +769,16 @@ bool gemv_silu_ok(int64_t N, int64_t K, int wbits) {
   return N % 64 == 0 && cpr <= 64 * 5;  // rows inside one wave (lanes per row <= 64)
 }
 
+size_t gemm_ws_need(int64_t M, int64_t N, int64_t K, int wbits) {
+  if (M > kSkinnyMaxRows) return gemm_ws_bytes(M, N, K, wbits);
+  return gemm_skinny_ok(M, K, wbits) ? skinny_ws_bytes(M, N, K, wbits) : 0;
+}
+
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes) {
   if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes);
-  if (gemm_skinny_ok(M, K, wbits)) return gemm_skinny_launch(x, w, sz, y, M, N, K, wbits, st);
+  if (gemm_skinny_ok(M, K, wbits))
+    return gemm_skinny_launch(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* yp = static_cast<uint16_t*>(y);
   for (int64_t m = 0; m < M; ++m) R4Q_TRY(gemv_launch(xp + m * K, w, sz, yp + m * N, N, K, wbits, st));
@@ -800,7 +806,7 @@ extern "C" int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbi
   R4Q_REQUIRE(M >= 1 && N >= 1 && K >= 32 && K % 32 == 0 &&
                   (wbits == 4 || wbits == 8 || wbits == 16),
               "gemm_workspace_bytes: bad shape or format");
-  *bytes = M > r4q::kSkinnyMaxRows ? r4q::gemm_ws_bytes(M, N, K, wbits) : 0;
+  *bytes = r4q::gemm_ws_need(M, N, K, wbits);
   return R4Q_OK;
 }
 
