@@ -422,7 +422,8 @@ def main():
 
     log("building synthetic model")
     t0 = time.time()
-    m = build_model(args.ctx, args.warmup + args.steps + 8, args.batch, dev)
+    # capacity for the decode steps and for the 512-token prompt leg below
+    m = build_model(args.ctx, max(args.warmup + args.steps + 8, 520 - args.ctx), args.batch, dev)
     log(f"model ready in {time.time() - t0:.1f} s (weights {m['wbytes'] / 1e9:.2f} GB + "
         f"LM head {m['lm_bytes'] / 1e9:.2f} GB)")
     h = (torch.randn(args.batch, 1, m["D"], generator=torch.Generator().manual_seed(1)) * 0.5).half().to(dev)
