@@ -25,7 +25,6 @@ namespace r4q {
 namespace {
 
 constexpr int kMaxSplits = 128;  // partials per (sequence, head)
-constexpr int kMergeChunk = 64;  // splits merged per round (one per lane)
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
 
 // ------------------------------------------------ MFMA flash-decode partials
@@ -455,6 +454,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 // Split merge, one wave per (query head, sequence); lane j owns dims 2j and
 // 2j+1.  Every load is issued before any arithmetic:
 //   m* = max_s m_s,  out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s.
+// CH splits per round (16, 32 or 64: the smallest covering the split count;
+// the slots past the last split add exact zeros, so CH does not change the
+// result).  Measured: 16 splits 4.56 us with CH = 64, 2.24 us with CH = 16.
+template <int CH>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part,
                                                         uint16_t* __restrict__ outp,
                                                         int64_t out_stride, int H, int nsplit) {
@@ -465,16 +468,16 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
   // splits in chunks of 64 (lane s holds split c0+s's m and l) with a
   // running maximum; every load of a chunk is issued before its arithmetic
   float M = -INFINITY, Ls = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int c0 = 0; c0 < nsplit; c0 += kMergeChunk) {
-    const int nc = min(kMergeChunk, nsplit - c0);
+  for (int c0 = 0; c0 < nsplit; c0 += CH) {
+    const int nc = min(CH, nsplit - c0);
     float ms = -INFINITY, ls = 0.f;
     if (lane < nc) {
       ms = pb[(int64_t)(c0 + lane) * kPart];
       ls = pb[(int64_t)(c0 + lane) * kPart + 1];
     }
-    float2 ov[kMergeChunk];
+    float2 ov[CH];
 #pragma unroll
-    for (int s = 0; s < kMergeChunk; ++s)
+    for (int s = 0; s < CH; ++s)
       ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(s, nc - 1)) * kPart + 4 +
                                                2 * lane);
     const float Mn = fmaxf(M, wave_max(ms));
@@ -484,7 +487,7 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
     a0 *= r;
     a1 *= r;
 #pragma unroll
-    for (int s = 0; s < kMergeChunk; ++s) {
+    for (int s = 0; s < CH; ++s) {
       const float ws = readlane_f(w, s);  // 0 past the chunk end
       a0 = __builtin_fmaf(ws, ov[s].x, a0);
       a1 = __builtin_fmaf(ws, ov[s].y, a1);
@@ -552,9 +555,19 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
 #undef R4Q_ATTN_MFMA
   if (!launched)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
-  if (nsplit > 1)
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)H, (unsigned)B), dim3(64), 0, st, part,
-                       static_cast<uint16_t*>(out), out_stride, (int)H, nsplit);
+  if (nsplit > 1) {
+    const dim3 mg((unsigned)H, (unsigned)B);
+    auto* o16 = static_cast<uint16_t*>(out);
+    if (nsplit <= 16)
+      hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         nsplit);
+    else if (nsplit <= 32)
+      hipLaunchKernelGGL(attn_merge_kernel<32>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         nsplit);
+    else
+      hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         nsplit);
+  }
   return launch_status("flash_decode");
 }
 
