@@ -407,7 +407,7 @@ def main():
         f"{rf_bytes} bytes: {rf_us:.2f} us")
 
     attn = {}
-    for c in (2048, 8192, 32768):
+    for c in (128, 2048, 8192, 32768):
         a_us, a_bytes = flash_decode_leg(dev, c)
         attn[str(c)] = {"us": round(a_us, 3), "kv_bytes": a_bytes,
                         "gbps": round(a_bytes / a_us / 1e3, 1),
