@@ -97,3 +97,40 @@ def test_fused_ops_surface_matches_reference_signatures():
     assert sig["fused_qknorm_rope_decode"] == ["q", "k", "q_norm_weight", "k_norm_weight", "cos",
                                                "sin", "position", "eps"]
     assert sig["fused_rope_decode"] == ["q", "k", "cos", "sin", "position"]
+
+
+def test_gemm_workspace_sizes():
+    """Host-side split policy: the skinny GEMM (2-16 rows) asks for S * M * N
+    fp32 of partials only where N is narrow (few 64-row tiles); wide N, one
+    row, and shapes off the ring's K step ask for none; M >= 256 follows the
+    tiled GEMM's plan."""
+    def ws(M, N, K, bits):
+        b = C.c_size_t(123)
+        R.call("r4q_gemm_workspace_bytes", M, N, K, bits, C.byref(b))
+        return b.value
+    for bits in (4, 8):
+        narrow = ws(8, 5120, 17408, bits)            # down: 80 tiles
+        assert narrow > 0 and narrow % (8 * 5120 * 4) == 0
+        assert 2 <= narrow // (8 * 5120 * 4) <= 8  # split count
+        assert ws(8, 34816, 5120, bits) == 0          # gate_up: enough tiles
+    assert ws(8, 151936, 5120, 16) == 0               # LM head
+    assert ws(1, 5120, 17408, 4) == 0                 # batch 1: GEMV, no workspace
+    assert ws(8, 5120, 17408 + 32, 4) == 0            # K off the ring step: per-row path
+    assert ws(512, 5120, 17408, 4) > 0                # tiled GEMM, split along K
+    with pytest.raises(RuntimeError):
+        ws(8, 5120, 100, 4)                           # K % 32 != 0
+
+
+def test_gate_up_silu_split_point():
+    """Whole 64-row units in multiples of 256 (the CU count), the rest as
+    fp32 pairs; fewer than 256 units: all units."""
+    def split(I):
+        v = C.c_int64(-1)
+        R.call("r4q_gate_up_silu_split", I, C.byref(v))
+        return v.value
+    assert split(17408) == 16384
+    assert split(8448) == 8192
+    assert split(1024) == 1024
+    assert split(96) == 96
+    with pytest.raises(RuntimeError):
+        split(100)
