@@ -35,7 +35,7 @@ sys.path.insert(0, PKG)
 METRIC = "INT4 GEMV HBM GB/s (% of peak); decode tok/s at ctx=2048, batch 1"
 HBM_PEAK_GBPS = 8000.0
 MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16
-ROOFLINE_KERNEL = "gemv_kernel<4, 32, 5, 1, false, false>"
+ROOFLINE_KERNEL = "gemv_kernel<4, 32, 5, 1, 0, 0>"
 # Counter-derived HBM bytes per launch of ROOFLINE_KERNEL (FETCH_SIZE + WRITE_SIZE
 # passes, calibrated against a copy of known size), written by that measurement.
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "int4_gemv_5120x17408_roofline.md")
