@@ -670,16 +670,30 @@ bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
   return M >= 2 && M <= 16 && K % ks == 0;
 }
 
-// Split count of the skinny ring: toward ~512 workgroups when the 64-row
-// tiles alone are fewer, each split keeping at least 8 K steps (measured at
-// M = 8: down 5120 x 17408 7 splits 23.6 us, 4: 26.1, none: 53.4; qkv
-// 7168 x 5120 2 splits 12.8 us, 5: 14.8, none: 17.5); S > 1 needs
-// S * M * N fp32 of workspace.
+// Split count of the skinny ring.  A CU streams its workgroups' weight
+// tiles at about the same rate whether it holds one or several, so the step
+// ends with the most-loaded CU: cost(S) = ceil(ntiles S / CUs) * kps + S,
+// the last term charging each split its fp32 partials and share of the
+// reduce.  S runs over 1..8 with at most 8 workgroups per CU (past that the
+// quantisation the model prices is smoothed out and splitting loses: FP16
+// 151936 x 5120 at M = 8, 2 splits 279 us against 268); ties go to more
+// splits.  Measured at M = 8 (us, chosen / unsplit / old rule): INT4 o
+// 5120 x 5120 3 splits 10.5 / 17.1 / 12.1, qkv 7168 x 5120 2: 12.9 / 17.8,
+// gate_up 34816 x 5120 3: 34.8 / 39.4, down 5120 x 17408 3: 23.1 / 51.6 /
+// 23.2; INT8 o 3: 11.5 / 18.7 / 13.1, qkv 2: 14.0 / 19.3 / 17.3, down 3:
+// 25.7 / 55.1 / 29.9.  S > 1 needs S * M * N fp32 of workspace.
 int skinny_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  constexpr int64_t kCUs = 256;  // MI355X
   const int64_t ntiles = (N + kSkTile - 1) / kSkTile;
   const int64_t kt = K / (1024 / wbits);
-  int64_t S = (512 + ntiles - 1) / ntiles;
-  S = std::min<int64_t>(S, std::min<int64_t>(kSkMaxSplits, kt / 8));
+  int64_t S = 1, best = INT64_MAX;
+  for (int64_t s = 1; s <= std::min<int64_t>(kSkMaxSplits, kt); ++s) {
+    const int64_t kps = (kt + s - 1) / s;
+    const int64_t se = (kt + kps - 1) / kps;  // splits left non-empty
+    if (se > 1 && ntiles * se > 8 * kCUs) break;
+    const int64_t c = (ntiles * se + kCUs - 1) / kCUs * kps + se;
+    if (c <= best) best = c, S = se;
+  }
   if (const char* e = getenv("R4Q_SKINNY_SPLITS")) S = atoi(e);  // tuning override
   if (S < 2) return 1;
   // every split non-empty
