@@ -116,6 +116,17 @@ R4Q_API int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbits,
 R4Q_API int r4q_gemm_ws(const void* x, const void* w, const void* sz, void* y,
                         int64_t M, int64_t N, int64_t K, int wbits, void* ws,
                         size_t ws_bytes, void* stream);
+/* Batched gate/up projection with the SiLU gate: y[M,I] fp16 =
+ * FWHT-32(silu(g) * u), [g; u] = x W^T over W's 2I rows [gate; up],
+ * bit-identical to r4q_gemm_ws into [M, 2I] followed by r4q_silu_mul_fwht
+ * (in/out strides 2I / I).  The split-K partial sum, the gate and the
+ * FWHT run in one kernel.  For 2 <= M <= 16 and I % 32 == 0 with a
+ * workspace of r4q_gemm_workspace_bytes(M, 2I, K) that splits K; other
+ * shapes are rejected.  Replaces the batched decode step's launch_gemv
+ * (gate_up) + silu_hadamard_ds pair (hip:1031-1051, hip:2508-2516). */
+R4Q_API int r4q_gemm_silu_fwht_ws(const void* x, const void* w, const void* sz, void* y,
+                                  int64_t M, int64_t I, int64_t K, int wbits, void* ws,
+                                  size_t ws_bytes, void* stream);
 
 /* y[N] = W x with x = FWHT32(fp16(a [+ b]) * rrms * gamma) (the activation
  * of r4q_res_rmsnorm_fwht / r4q_rmsnorm_fwht, bit-identical) computed inside

@@ -232,6 +232,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
       prof.mark(st, kGemv);
       R4Q_TRY(gemv_fwht_launch(bf.y, hp, split, y.down_w, y.down_s, bf.d, D, I, y.down_bits, st));
     } else {
+      bool gated = false;
       if (fused) {
         R4Q_TRY(gemv_norm_launch(bf.o, bf.h, y.post_norm, bf.r, eps, y.gu_w, y.gu_s, bf.gu,
                                  2 * I, D, y.gu_bits, st));
@@ -239,10 +240,19 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
         prof.mark(st, kNorm);
         R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
         prof.mark(st, kGemv);
-        R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st, bf));
+        if (gemm_skinny_silu_ok(B, I, D, y.gu_bits, bf.ws_bytes)) {
+          // split-K skinny GEMM whose reduce applies the SiLU gate + FWHT-32
+          R4Q_TRY(gemm_skinny_silu_launch(bf.rot, y.gu_w, y.gu_s, bf.y, B, I, D, y.gu_bits, st,
+                                          bf.ws, bf.ws_bytes));
+          gated = true;
+        } else {
+          R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st, bf));
+        }
       }
-      prof.mark(st, kNorm);
-      R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
+      if (!gated) {
+        prof.mark(st, kNorm);
+        R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
+      }
       prof.mark(st, kGemv);
       R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st, bf));
     }

@@ -663,6 +663,49 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(const float* __
   Y[(int64_t)m * N + n] = f2h(v);
 }
 
+// Split sum fused with the SiLU gate of a gate/up projection (N = 2I
+// columns: gate 0..I-1, up I..2I-1).  Thread c of row m sums the 32 gate and
+// 32 up columns of chunk c over the splits in order and rounds each sum to
+// fp16 (what gemm_skinny_reduce_kernel stores), then stores
+// FWHT-32(silu(g) * u) in fp16 as silu_kernel<true> does.  64-thread
+// workgroups: a row holds only I / 32 chunks.
+__device__ __forceinline__ void skinny_sum32(const float* __restrict__ p, int64_t plane, int S,
+                                             float* v) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 t = q[i];
+    v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
+  }
+  for (int z = 1; z < S; ++z) {
+    q = reinterpret_cast<const float4*>(p + z * plane);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 t = q[i];
+      v[4 * i] += t.x, v[4 * i + 1] += t.y, v[4 * i + 2] += t.z, v[4 * i + 3] += t.w;
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void gemm_skinny_reduce_silu_kernel(
+    const float* __restrict__ part, uint16_t* __restrict__ Y, int M, int I, int S) {
+#pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
+  const int c = blockIdx.x * 64 + threadIdx.x, m = blockIdx.y;
+  if (c * 32 >= I) return;
+  const int64_t plane = (int64_t)M * 2 * I;
+  const float* pg = part + (int64_t)m * 2 * I + c * 32;
+  float a[32], b[32];
+  skinny_sum32(pg, plane, S, a);
+  skinny_sum32(pg + I, plane, S, b);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float g = h2f(f2h(a[i])), u = h2f(f2h(b[i]));
+    a[i] = g / (1.0f + expf(-g)) * u;
+  }
+  fwht32(a);
+  store32h(Y + (int64_t)m * I + c * 32, a);
+}
+
 }  // namespace
 
 bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
@@ -708,9 +751,11 @@ size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
   return S > 1 ? (size_t)S * M * N * 4 : 0;
 }
 
-int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
-                       int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
-                       size_t ws_bytes) {
+namespace {
+// silu_I > 0: N = 2 silu_I gate/up columns, split (S > 1, checked by the
+// caller) and reduced by gemm_skinny_reduce_silu_kernel into y (M x silu_I).
+int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
+               int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes, int64_t silu_I) {
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
@@ -740,12 +785,37 @@ int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, in
   }
 #undef R4Q_SKINNY
   R4Q_TRY(launch_status("gemm_skinny"));
-  if (S > 1) {
+  if (silu_I > 0) {
+    hipLaunchKernelGGL(gemm_skinny_reduce_silu_kernel,
+                       dim3((unsigned)((silu_I / 32 + 63) / 64), (unsigned)M), dim3(64), 0, st,
+                       part, yp, (int)M, (int)silu_I, S);
+    R4Q_TRY(launch_status("gemm_skinny_reduce_silu"));
+  } else if (S > 1) {
     hipLaunchKernelGGL(gemm_skinny_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M),
                        dim3(256), 0, st, part, yp, (int)M, (int)N, S);
     R4Q_TRY(launch_status("gemm_skinny_reduce"));
   }
   return R4Q_OK;
+}
+}  // namespace
+
+int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                       int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
+                       size_t ws_bytes) {
+  return skinny_run(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes, 0);
+}
+
+bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes) {
+  return gemm_skinny_ok(M, K, wbits) && I > 0 && I % 32 == 0 &&
+         skinny_splits(M, 2 * I, K, wbits, ws_bytes) > 1;
+}
+
+int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                            int64_t I, int64_t K, int wbits, hipStream_t st, void* ws,
+                            size_t ws_bytes) {
+  R4Q_REQUIRE(gemm_skinny_silu_ok(M, I, K, wbits, ws ? ws_bytes : 0),
+              "gate_up_silu: shape or workspace does not take the split path");
+  return skinny_run(x, w, sz, y, M, 2 * I, K, wbits, st, ws, ws_bytes, I);
 }
 
 bool gemm_ring_ok(int64_t M, int wbits) { return M >= RBM && wbits != 16; }

@@ -820,6 +820,22 @@ extern "C" int r4q_gemm_ws(const void* x, const void* w, const void* sz, void* y
   return r4q::gemm_launch(x, w, sz, y, M, N, K, wbits, r4q::as_stream(stream), ws, ws_bytes);
 }
 
+extern "C" int r4q_gemm_silu_fwht_ws(const void* x, const void* w, const void* sz, void* y,
+                                     int64_t M, int64_t I, int64_t K, int wbits, void* ws,
+                                     size_t ws_bytes, void* stream) {
+  R4Q_REQUIRE(M >= 1 && I >= 1, "gemm_silu_fwht: bad shape");
+  R4Q_TRY(r4q::gemv_check(x, w, sz, y, 2 * I, K, wbits));
+  R4Q_REQUIRE(ws || ws_bytes == 0, "gemm_silu_fwht: workspace size without a workspace");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0,
+              "gemm_silu_fwht: workspace must be 16-byte aligned");
+  R4Q_REQUIRE(r4q::gemm_skinny_silu_ok(M, I, K, wbits, ws ? ws_bytes : 0),
+              "gemm_silu_fwht: M = %lld, I = %lld, K = %lld does not take the split skinny path "
+              "(2 <= M <= 16, I %% 32 == 0, workspace of r4q_gemm_workspace_bytes(M, 2I, K))",
+              (long long)M, (long long)I, (long long)K);
+  return r4q::gemm_skinny_silu_launch(x, w, sz, y, M, I, K, wbits, r4q::as_stream(stream), ws,
+                                      ws_bytes);
+}
+
 extern "C" int r4q_res_rmsnorm_fwht_gemv(const void* a, const void* b, const void* gamma,
                                          void* res_out, float eps, const void* w, const void* sz,
                                          void* y, int64_t N, int64_t K, int wbits,

@@ -62,6 +62,14 @@ size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits);
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                        int64_t N, int64_t K, int wbits, hipStream_t st, void* ws = nullptr,
                        size_t ws_bytes = 0);
+// The same GEMM over N = 2I gate/up columns with the SiLU gate and FWHT-32
+// fused into the split sum: y (M x I fp16) = FWHT-32(silu(gate) * up),
+// equal to the plain GEMM followed by silu_mul_fwht.  Needs the split path
+// (gemm_skinny_silu_ok).
+bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes);
+int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                            int64_t I, int64_t K, int wbits, hipStream_t st, void* ws,
+                            size_t ws_bytes);
 
 // Workspace bytes gemm_launch can use for a shape (0: none), over both the
 // skinny (M <= 16) and the tiled paths.

@@ -69,6 +69,7 @@ SIGNATURES = {
     "r4q_prefill_attention": [_p, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_gemm_workspace_bytes": [_i64, _i64, _i64, C.c_int, C.POINTER(C.c_size_t)],
     "r4q_gemm_ws": [_p, _p, _p, _p, _i64, _i64, _i64, C.c_int, _p, C.c_size_t, _p],
+    "r4q_gemm_silu_fwht_ws": [_p, _p, _p, _p, _i64, _i64, _i64, C.c_int, _p, C.c_size_t, _p],
     "r4q_rmsnorm": [_p, _p, _p, _i64, _i64, _f32, _p],
     "r4q_res_rmsnorm": [_p, _p, _p, _p, _p, _i64, _i64, _f32, _p],
     "r4q_rmsnorm_fwht": [_p, _p, _p, _i64, _i64, _f32, _p],
