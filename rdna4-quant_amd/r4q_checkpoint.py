@@ -7,14 +7,21 @@ Produces the int4_hip argument lists directly, so a real checkpoint runs
 through this library's kernels:
   * INT4 groups `{g}_packed` [N, K/2] u8 + `{g}_scales` [N, K/32] + `{g}_zeros`
     [N, K/32] u8 -> (packed, interleaved (scale, zero) fp16 [N, K/16])
-    (interleave_scale_zero, int4_engine_v5.py:95-102); a group without zeros
-    is symmetric two's-complement INT4 and becomes unsigned nibbles with zero
-    point 8 (convert_symmetric_to_asymmetric, :105-118);
+    (interleave_scale_zero, int4_engine_v5.py:95-102).  The writers store
+    `{g}_zeros` for every INT4 group (quantize_v4_gptq.py:397-403,
+    quantize_v5_pure_int4.py:353-358); the tag `{g}_precision` tells the two
+    formats apart: 'int4a' is asymmetric (unsigned nibbles, zero points as
+    stored), 'int4' symmetric (two's-complement nibbles, zeros all 0,
+    int4_quant_v2.py:240-247), which becomes unsigned nibbles with zero point
+    8 (convert_symmetric_to_asymmetric, int4_engine_v5.py:105-118).  Without
+    a tag, meta['use_asymmetric'] decides, and without that a missing zeros
+    key means symmetric;
   * INT8 groups `{g}_weights` [N, K] int8 + `{g}_scales` (symmetric, the v4
     format the reference engine cannot run) -> uint8 q + 128 with zero point
     128 in the same interleaved table, which the INT8 GEMV consumes;
   * lm_head.pt: asymmetric (packed, scales, zeros) or symmetric INT4
-    (packed, scales), converted the same way;
+    (packed, scales; quant_format 'int4_symmetric'), converted the same way
+    (int4_engine_v5.py:163-176);
   * norms, embedding and final norm cast to fp16.
 Every file is read with torch.load(weights_only=True): tensors, numbers,
 strings and dicts only, nothing executed from the file.
@@ -48,12 +55,25 @@ def sym_int4_to_asym(packed: torch.Tensor):
     return ((lo & 0x0F) | ((hi & 0x0F) << 4)).to(torch.uint8)
 
 
-def _int4_group(packed, scales, zeros, device):
+def int4_is_symmetric(precision, zeros, meta) -> bool:
+    """Symmetric (two's-complement) or asymmetric INT4 group: the writer's
+    `{g}_precision` tag first ('int4' symmetric, 'int4a' asymmetric), then
+    the checkpoint-wide meta['use_asymmetric'], then a missing zeros key."""
+    if precision in ("int4", "int4a"):
+        return precision == "int4"
+    if meta is not None and "use_asymmetric" in meta:
+        return not bool(meta["use_asymmetric"])
+    return zeros is None
+
+
+def _int4_group(packed, scales, zeros, symmetric, device):
     N = packed.shape[0]
     nb = scales.shape[1]
-    if zeros is None:
+    if symmetric:
         packed = sym_int4_to_asym(packed)
         zeros = torch.full((N, nb), 8, dtype=torch.uint8)
+    elif zeros is None:
+        raise ValueError("asymmetric INT4 group without zero points")
     return (packed.contiguous().to(device),
             interleave_scale_zero(scales, zeros).to(device).contiguous())
 
@@ -65,11 +85,13 @@ def _int8_group(weights, scales, device):
 
 
 def rope_tables(head_dim: int, n_pos: int, theta: float, device):
-    """cos/sin [n_pos, head_dim/2] fp16 (precompute_rope_freqs,
-    engine_utils.py:70-76)."""
-    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
-    ang = torch.outer(torch.arange(n_pos, dtype=torch.float64), inv)
-    return ang.cos().half().to(device), ang.sin().half().to(device)
+    """cos/sin [n_pos, head_dim/2] fp16, built as precompute_rope_freqs does
+    (engine_utils.py:70-76): float32 frequencies and angles on `device`,
+    cos/sin in float32, then rounded to fp16."""
+    freqs = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    t = torch.arange(n_pos, device=device).float()
+    ang = torch.outer(t, freqs)
+    return ang.cos().half(), ang.sin().half()
 
 
 class QuantizedModel:
@@ -123,9 +145,10 @@ def load_quantized(quant_dir, device="cuda", max_seq: int = 2048,
                 w, s = _int8_group(ld[f"{g}_weights"], ld[f"{g}_scales"], m.device)
                 prec[g] = "int8"
             else:
-                w, s = _int4_group(ld[f"{g}_packed"], ld[f"{g}_scales"], ld.get(f"{g}_zeros"),
-                                   m.device)
-                prec[g] = "int4"
+                zeros = ld.get(f"{g}_zeros")
+                sym = int4_is_symmetric(ld.get(f"{g}_precision"), zeros, meta)
+                w, s = _int4_group(ld[f"{g}_packed"], ld[f"{g}_scales"], zeros, sym, m.device)
+                prec[g] = "int4" if sym else "int4a"
             getattr(m, a + "_w").append(w)
             getattr(m, a + "_s").append(s)
             getattr(m, a + "_N").append(int(ld[f"{g}_N"]))
@@ -135,7 +158,8 @@ def load_quantized(quant_dir, device="cuda", max_seq: int = 2048,
         del ld
     lm = _load(d / "lm_head.pt")
     m.lm_N, m.lm_K = int(lm["N"]), int(lm["K"])
-    m.lm_w, m.lm_s = _int4_group(lm["packed"], lm["scales"], lm.get("zeros"), m.device)
+    lm_sym = "zeros" not in lm or lm.get("quant_format") == "int4_symmetric"
+    m.lm_w, m.lm_s = _int4_group(lm["packed"], lm["scales"], lm.get("zeros"), lm_sym, m.device)
     m.embed = _load(d / "embed.pt").to(torch.float16).contiguous().to(m.device)
     m.final_norm = _load(d / "final_norm.pt").to(torch.float16).contiguous().to(m.device)
     m.vocab = m.embed.shape[0]

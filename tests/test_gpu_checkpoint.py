@@ -1,6 +1,7 @@
 """A checkpoint directory in the reference's on-disk layout, loaded by
 r4q_checkpoint, runs through int4_hip: prompt pass and a decode step agree
-with the oracle built from the same loaded tensors (rel-L2 <= 5e-3)."""
+with the oracle built from the same loaded tensors (rel-L2 <= 5e-3), for
+asymmetric ('int4a') and symmetric ('int4', --symmetric) INT4 files."""
 import numpy as np
 import pytest
 import torch
@@ -42,8 +43,9 @@ def _common(m):
                 lm_bits=4)
 
 
-def test_checkpoint_prefill_then_decode(dev, tmp_path):
-    write_fake_checkpoint(tmp_path, seed=3)
+@pytest.mark.parametrize("symmetric", [False, True])
+def test_checkpoint_prefill_then_decode(dev, tmp_path, symmetric):
+    write_fake_checkpoint(tmp_path, seed=3, symmetric=symmetric)
     m = CK.load_quantized(tmp_path, device=dev, max_seq=32)
     layers = _oracle_layers(m)
     ids = np.random.default_rng(1).integers(0, m.vocab, 9)
