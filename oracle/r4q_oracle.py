@@ -46,12 +46,17 @@ PINNING = {
                          "pos 0 identity",
     "flash_decode": "torch F.scaled_dot_product_attention(enable_gqa=True) on the "
                     "decoded cache (int4_engine_v5.py:245); seq_len 1 closed form",
-    "decode_step": "composition of the pinned functions; layer-by-layer hidden "
-                   "state checks",
+    "decode_step": "composition of the pinned functions; equals row m of "
+                   "prefill_logits(attend_fp8=True) at position m on the same caches "
+                   "(rel-L2 <= 5e-3, logits and every layer's hidden state)",
+    "decode_step_batch": "row b equals decode_step on row b (same functions, "
+                         "projections over all rows at once)",
     "attention_prefill": "torch F.scaled_dot_product_attention(is_causal=True, "
                          "enable_gqa=True) (hip:2262-2264); M=1 closed form (= v)",
-    "prefill_logits": "composition of the pinned functions; row m of the prompt pass "
-                      "equals the decode step at position m on the same caches",
+    "prefill_logits": "composition of the pinned functions; a torch restatement of "
+                      "the reference's own prompt pass (fast_prefill, "
+                      "int4_engine_v5.py:214-266) matches every layer's hidden state "
+                      "and the logits (rel-L2 <= 5e-3, norm weights 0.5-1.5)",
     "sample_top_p": "kept set vs a literal torch restatement of the reference's top-p "
                     "code (int4_engine_v5.py:387-399: sort, cumsum, mask) in float64; "
                     "draw frequencies vs the renormalised kept distribution "
@@ -481,10 +486,60 @@ def decode_step(layers, hidden16, pos: int, k_caches, v_caches, *, H, Hk, D, hid
     return h, logits
 
 
+def decode_step_batch(layers, hidden16, pos: int, k_caches, v_caches, *, H, Hk, D, hidden,
+                      inter, eps, rope_cos, rope_sin, final_norm=None, lm_w=None, lm_s=None,
+                      lm_bits=4, k_scales=None, v_scales=None, forced_kv=None, kv_trace=None):
+    """decode_step for B independent sequences at one position (the batched
+    step of hip:2343-2528 with one row per sequence): hidden16 [B, hidden];
+    k_caches/v_caches[li] are [B, Hk, max_seq, D] uint8, mutated at `pos`.
+    Each projection dequantises its weights once for all rows; the per-row
+    steps (head norm + RoPE + FP8 write, attention) loop over the rows, so
+    row b equals decode_step on row b.  forced_kv[li] = (k_bytes, v_bytes)
+    [B, Hk, D]; kv_trace receives per layer (own_k, own_v, k_pre, v_pre)
+    [B, Hk, D].  Returns (hidden16 [B, hidden], logits16 [B, lm_N] or None)."""
+    h = np.asarray(hidden16, np.float16).reshape(-1, hidden)
+    B = h.shape[0]
+    L = len(layers)
+    rot = rmsnorm_fwht(h, layers[0].in_norm, eps)
+    for li, ly in enumerate(layers):
+        qkv = gemm(rot, ly.qkv_w, ly.qkv_s, ly.qkv_bits)
+        ks = None if k_scales is None else k_scales[li]
+        vs = None if v_scales is None else v_scales[li]
+        att = np.empty((B, H * D), np.float16)
+        own = [np.empty((B, Hk, D), np.uint8) for _ in range(2)]
+        pre = [np.empty((B, Hk, D), np.float32) for _ in range(2)]
+        for b in range(B):
+            q_out, _, kb, vb, kpre, vpre = head_norm_rope_kv(
+                qkv[b], ly.q_norm, ly.k_norm, rope_cos, rope_sin, pos, H, Hk, D, eps, ks, vs,
+                return_prequant=True)
+            own[0][b], own[1][b], pre[0][b], pre[1][b] = kb, vb, kpre, vpre
+            if forced_kv is not None:
+                kb, vb = forced_kv[li][0][b], forced_kv[li][1][b]
+            k_caches[li][b, :, pos, :] = kb
+            v_caches[li][b, :, pos, :] = vb
+            att[b] = attention_decode(q_out, k_caches[li][b], v_caches[li][b], pos + 1, H, Hk, D,
+                                      ks, vs, fwht=True)
+        if kv_trace is not None:
+            kv_trace.append((own[0], own[1], pre[0], pre[1]))
+        o = gemm(att, ly.o_w, ly.o_s, ly.o_bits)
+        rot, r = res_rmsnorm_fwht(o, h, ly.post_norm, eps)
+        gu = gemm(rot, ly.gu_w, ly.gu_s, ly.gu_bits)
+        y = silu_mul_fwht(gu[:, :inter], gu[:, inter:])
+        d = gemm(y, ly.down_w, ly.down_s, ly.down_bits)
+        nxt = layers[li + 1].in_norm if li + 1 < L else layers[0].in_norm
+        rot, h = res_rmsnorm_fwht(d, r, nxt, eps)
+    logits = None
+    if final_norm is not None:
+        rot = rmsnorm_fwht(h, final_norm, eps)
+        logits = gemm(rot, lm_w, lm_s, lm_bits)
+    return h, logits
+
+
 # ------------------------------------------------------------------------ a15
 def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos, rope_sin,
                    final_norm=None, lm_w=None, lm_s=None, lm_bits=4, k_caches=None,
-                   v_caches=None, k_scales=None, v_scales=None, kv_trace=None):
+                   v_caches=None, k_scales=None, v_scales=None, kv_trace=None, trace=None,
+                   attend_fp8=False):
     """Prompt pass over token ids [M] (int4_prefill_logits hip:2127-2320):
     embedding, then per layer RMSNorm + FWHT, QKV, per-row head RMSNorm +
     RoPE at position m, causal attention + FWHT, O, residual + norm + FWHT,
@@ -494,7 +549,12 @@ def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos
     uint8 per layer) the FP8 codes of positions 0..M-1 are written (K from
     the float32 rotated values, as int4_engine_v5.py:237-242 fills the cache
     for decode); kv_trace receives per layer (k_bytes, v_bytes, k_pre, v_pre)
-    [M, Hk, D].  Returns (hidden16 [M, hidden], logits16 [M, lm_N] or None)."""
+    [M, Hk, D] and `trace` the residual stream [M, hidden] after each layer.
+    attend_fp8=True makes the attention read K and V through their FP8 codes
+    (decoded, scaled and held as fp16, exact at scale 1) as the decode step
+    does, instead of the fp16 values (the reference prompt pass,
+    int4_engine_v5.py:245).  Returns (hidden16 [M, hidden], logits16
+    [M, lm_N] or None)."""
     ids = np.asarray(ids, np.int64).reshape(-1)
     M = ids.size
     x = np.asarray(embed, np.float16)[ids]
@@ -524,6 +584,11 @@ def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos
         if k_caches is not None:
             k_caches[li][:, :M, :] = kb_all.transpose(1, 0, 2)
             v_caches[li][:, :M, :] = vb_all.transpose(1, 0, 2)
+        if attend_fp8:
+            ksc = np.ones(Hk) if ks is None else np.asarray(ks, np.float64)
+            vsc = np.ones(Hk) if vs is None else np.asarray(vs, np.float64)
+            k = (fp8_decode_ref(kb_all) * ksc[None, :, None]).astype(np.float16)
+            v = (fp8_decode_ref(vb_all) * vsc[None, :, None]).astype(np.float16)
         rot = attention_prefill(q, k, v, H, Hk, fwht=True)
         o = gemm(rot, ly.o_w, ly.o_s, ly.o_bits)
         rot, r = res_rmsnorm_fwht(o, x, ly.post_norm, eps)
@@ -535,6 +600,8 @@ def prefill_logits(layers, ids, embed, *, H, Hk, D, hidden, inter, eps, rope_cos
         else:
             nxt = final_norm if final_norm is not None else layers[0].in_norm
         rot, x = res_rmsnorm_fwht(d, r, nxt, eps)
+        if trace is not None:
+            trace.append(x.copy())
     logits = None
     if final_norm is not None:
         logits = gemm(rot, lm_w, lm_s, lm_bits)
