@@ -61,60 +61,16 @@ def log(msg):
 
 
 def build_model(ctx, extra, batch, dev):
-    import torch
-
-    import int4_hip
     import r4q_synth as S
-
-    c = S.QWEN3_14B
-    D, I, H, Hk, hd, L, V = c["hidden"], c["inter"], c["heads"], c["kv_heads"], c["head_dim"], \
-        c["layers"], c["vocab"]
-    g = S.gen(4, dev)
-    mask = S.precision_mask(L, seed=4)
-    args = {k: [] for k in ("qkv_w", "qkv_s", "qkv_N", "o_w", "o_s", "o_N", "gu_w", "gu_s", "gu_N",
-                            "down_w", "down_s", "down_N", "in_norm", "post_norm", "q_norm",
-                            "k_norm")}
-    wbytes = 0
-    for li in range(L):
-        bits = {n: mask[(li, n)] for n in ("qkv", "o", "gu", "down")}
-        ly = S.make_layer(D, I, H, Hk, hd, g, device=dev, bits=bits)
-        for k in args:
-            args[k].append(ly[k])
-        for n in ("qkv", "o", "gu", "down"):
-            N = ly[n + "_N"]
-            K = {"qkv": D, "o": H * hd, "gu": D, "down": I}[n]
-            wbytes += N * K * ly[n + "_bits"] // 8 + N * (K // 32) * 3
-        if (li + 1) % 10 == 0:
-            log(f"layer {li + 1}/{L} generated")
-    max_seq = ctx + extra
-    kc, vc = [], []
-    for li in range(L):
-        k = torch.zeros(batch, Hk, max_seq, hd, dtype=torch.uint8, device=dev)
-        v = torch.zeros_like(k)
-        k[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev, batch))
-        v[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev, batch))
-        kc.append(k)
-        vc.append(v)
-    cos, sin = S.rope_tables(hd, max_seq, c["rope_theta"], dev)
-    final_norm = S.norm_weight(D, g, dev)
-    lm_w, _ = S.fp16_weight(V, D, g, dev)
-    embed, _ = S.fp16_weight(V, D, g, dev)
+    m = S.qwen3_model(ctx, extra, batch, dev, log=log)
+    import torch
     torch.cuda.synchronize()
-    m = dict(args=args, kc=kc, vc=vc, cos=cos, sin=sin, final_norm=final_norm, lm_w=lm_w,
-             embed=embed, D=D, I=I, H=H, Hk=Hk, hd=hd, L=L, V=V, eps=c["eps"], mask=mask,
-             max_seq=max_seq, wbytes=wbytes, lm_bytes=V * D * 2)
     return m
 
 
 def bench_args(m, start_pos):
-    import torch
-    a = m["args"]
-    had = torch.zeros(32, 32, dtype=torch.float16, device=m["lm_w"].device)
-    return (a["qkv_w"], a["qkv_s"], a["qkv_N"], a["o_w"], a["o_s"], a["o_N"], a["gu_w"],
-            a["gu_s"], a["gu_N"], a["down_w"], a["down_s"], a["down_N"], a["in_norm"],
-            a["post_norm"], a["q_norm"], a["k_norm"], m["cos"], m["sin"], start_pos, m["H"],
-            m["Hk"], m["hd"], m["D"], m["I"], m["eps"], m["kc"], m["vc"], m["final_norm"],
-            m["lm_w"], None, m["V"], m["D"], had)
+    import r4q_synth as S
+    return S.qwen3_bench_args(m, start_pos)
 
 
 def gemv_roofline(dev, iters=200, copies=8, eager_tail=0):

@@ -42,7 +42,11 @@
  *   r4q_rope             <- dbg_rope                (:3506-3522)
  *   r4q_head_norm_rope_kv<- head_rmsnorm_rope_kv    (:1620-1683)
  *   r4q_flash_decode     <- launch_flash_decode     (:1547-1593)
+ *   r4q_flash_decode_qkv <- head_rmsnorm_rope_kv + launch_flash_decode
+ *                           pair of the decode step (:1620-1683, :2487-2500)
  *   r4q_decode_step      <- decode_step / decode_step_logits (:2343-2595)
+ *   r4q_decode_step_graph <- the same, as called once per token by the engine
+ *                           (int4_engine_v5.py:272), replayed from a hipGraph
  *   r4q_decode_bench     <- decode_bench / decode_bench_graph (:2601-3041),
  *                           and decode_loop (:3284-3466) via tokens_out
  *   r4q_decode_profile   <- decode_profile          (:3047-3273)
@@ -244,6 +248,22 @@ R4Q_API int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
                      int64_t B, int64_t H, int64_t Hk, int64_t D,
                      int64_t max_seq, int64_t seq_len, int fwht, void* stream);
 
+/* The decode step's attention with its fused prologue, for one new position
+ * `pos` of B sequences: qkv row b (at qkv + b*qkv_stride) holds the raw QKV
+ * projection (q [H,D] | k [Hk,D] | v [Hk,D]); the kernel applies the
+ * per-head RMSNorm + RoPE of r4q_head_norm_rope_kv to q and k (bit-identical
+ * arithmetic), writes the FP8 codes of k and v at `pos` into the caches, and
+ * attends over positions 0..pos (the split count follows the cache capacity
+ * max_seq, as in the decode step).  out as r4q_flash_decode.  Replaces the
+ * head_rmsnorm_rope_kv -> launch_flash_decode pair of the reference's decode
+ * step (hip:1620-1683, hip:1547-1593, called at hip:2487-2500). */
+R4Q_API int r4q_flash_decode_qkv(r4q_ctx* ctx, const void* qkv, int64_t qkv_stride,
+                                 const void* q_norm, const void* k_norm, const void* cos_t,
+                                 const void* sin_t, float eps, void* k_cache, void* v_cache,
+                                 const float* k_scale, const float* v_scale, void* out,
+                                 int64_t B, int64_t H, int64_t Hk, int64_t D, int64_t max_seq,
+                                 int64_t rope_len, int64_t pos, int fwht, void* stream);
+
 /* ----------------------------------------------------------- decode model */
 
 /* One decoder layer's tensors.  *_bits is 4, 8 or 16 per matrix.
@@ -279,6 +299,23 @@ typedef struct r4q_model {
 R4Q_API int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                     int64_t B, int64_t pos, void* hidden_out, void* logits,
                     void* stream);
+/* r4q_decode_step replayed from a captured hipGraph: the first call for a
+ * (model, B, buffers) combination captures the step with the position held
+ * in device memory, later calls at any position set that position and replay
+ * it (about 250 launches become one).  Bit-identical results to
+ * r4q_decode_step.  Replaces the per-token decode_step_logits call of the
+ * engine (int4_engine_v5.py:272 -> hip:2534-2595).  Must not be called while
+ * the caller's stream is being captured. */
+R4Q_API int r4q_decode_step_graph(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                                  int64_t B, int64_t pos, void* hidden_out, void* logits,
+                                  void* stream);
+/* How the decode step runs a model at batch B, without running it (no
+ * counterpart in the reference; for tests and measurement):
+ * out[0] = attention split count (from the cache capacity),
+ * out[1] = layers whose gate/up projection applies the SiLU gate + FWHT-32
+ * in the same launch (batch 1: the GEMV's SiLU epilogue; batch > 1: the
+ * split-K reduce of the skinny GEMM).  n >= 2. */
+R4Q_API int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int64_t n);
 /* Run `num_tokens` steps from start_pos.  use_graph != 0 captures one step
  * into a hipGraph and replays it with the position held in device memory.
  * Greedy next token (argmax + embedding gather) runs on the device between
@@ -310,6 +347,18 @@ R4Q_API int r4q_sample(r4q_ctx* ctx, const void* logits, int64_t B, int64_t V, i
  * out_ms[5] = {total, gemv, attention, norm, rest}. */
 R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                        int64_t pos, float* out_ms, void* stream);
+
+/* Measurement aid with no counterpart in the reference: overrides one
+ * launch-shape choice for the whole process (value 0 restores the built-in
+ * choice).  Knobs: "gemv_lpr" (lanes per GEMV row: 16..256, power of two),
+ * "gemv_wgs" (GEMV workgroup cap, 1..65536), "gemv_ub" (GEMV steps per batch,
+ * 1..2), "attn_splits" (flash-decode splits, 1..128), "skinny_splits"
+ * (skinny GEMM K splits, 1..8), "gemm_splits" (ring GEMM K splits of every
+ * tile, 1..16).  Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS,
+ * R4Q_GEMV_UB, R4Q_ATTN_SPLITS, R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, read once.
+ * Results do not depend on these choices beyond fp32 summation order
+ * (split counts) -- they exist for sweeps and tests. */
+R4Q_API int r4q_tune(const char* name, int value);
 
 /* Measurement aid with no counterpart in the reference: reads `bytes` bytes
  * at src (16-byte aligned) once, with the fastest plain-read layout measured

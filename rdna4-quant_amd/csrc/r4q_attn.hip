@@ -17,6 +17,8 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <atomic>
+
 #include "r4q_ctx.hpp"
 #include "r4q_device.hpp"
 #include "r4q_host.hpp"
@@ -508,10 +510,7 @@ int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
   // (32 splits against 64: 10.5 vs 10.9 us at 8K, 18.3 vs 19.0 us at 32K).
   // Depends only on the cache capacity, so a captured graph stays valid as
   // the sequence grows.
-  if (const char* e = getenv("R4Q_ATTN_SPLITS")) {  // tuning override
-    const int v = atoi(e);
-    if (v >= 1 && v <= kMaxSplits) return v;
-  }
+  if (const int v = tuning().attn_splits.load()) return v;  // measurement override (r4q_tune)
   int64_t n = (cap_len + 127) / 128;
   if (n > 32) n = 32;
   const int64_t by_wg = 512 / (B * Hk > 0 ? B * Hk : 1);
@@ -572,8 +571,15 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   return launch_status("flash_decode");
 }
 
+namespace {
+std::atomic<uint64_t> g_devbuf_epoch{0};
+}
+
+uint64_t devbuf_epoch() { return g_devbuf_epoch.load(std::memory_order_relaxed); }
+
 int DevBuf::reserve(size_t need) {
   if (need <= bytes) return R4Q_OK;
+  g_devbuf_epoch.fetch_add(1, std::memory_order_relaxed);
   if (ptr) {
     (void)hipFree(ptr);
     ptr = nullptr;
@@ -589,6 +595,7 @@ int DevBuf::reserve(size_t need) {
 }
 
 void DevBuf::release() {
+  if (ptr) g_devbuf_epoch.fetch_add(1, std::memory_order_relaxed);
   if (ptr) (void)hipFree(ptr);
   ptr = nullptr;
   bytes = 0;
@@ -616,4 +623,32 @@ extern "C" int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
   return r4q::launch_flash_decode(q, q_stride, k_cache, v_cache, k_scale, v_scale, out, H * D, B,
                                   H, Hk, max_seq, seq_len, nullptr, nsplit, fwht,
                                   static_cast<float*>(ctx->attn.ptr), r4q::as_stream(stream));
+}
+
+extern "C" int r4q_flash_decode_qkv(r4q_ctx* ctx, const void* qkv, int64_t qkv_stride,
+                                    const void* q_norm, const void* k_norm, const void* cos_t,
+                                    const void* sin_t, float eps, void* k_cache, void* v_cache,
+                                    const float* k_scale, const float* v_scale, void* out,
+                                    int64_t B, int64_t H, int64_t Hk, int64_t D, int64_t max_seq,
+                                    int64_t rope_len, int64_t pos, int fwht, void* stream) {
+  R4Q_REQUIRE(ctx, "flash_decode_qkv: null context");
+  R4Q_REQUIRE(qkv && q_norm && k_norm && cos_t && sin_t && k_cache && v_cache && out,
+              "flash_decode_qkv: null pointer");
+  R4Q_REQUIRE(D == 128, "flash_decode_qkv: head_dim must be 128");
+  R4Q_REQUIRE(B >= 1 && H >= 1 && Hk >= 1 && H % Hk == 0, "flash_decode_qkv: bad head counts");
+  R4Q_REQUIRE(pos >= 0 && pos < max_seq && pos < rope_len,
+              "flash_decode_qkv: pos %lld outside the cache (%lld) or RoPE table (%lld rows)",
+              (long long)pos, (long long)max_seq, (long long)rope_len);
+  R4Q_REQUIRE(qkv_stride >= (H + 2 * Hk) * D, "flash_decode_qkv: qkv stride < (H + 2 Hk) * D");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15) == 0,
+              "flash_decode_qkv: out must be 16-byte aligned");
+  // split count from the cache capacity, as in the decode step
+  const int nsplit = r4q::attn_num_splits(max_seq, B, Hk);
+  R4Q_TRY(ctx->attn.reserve(r4q::attn_ws_bytes(B, H, nsplit)));
+  const r4q::AttnQK qk{static_cast<const uint16_t*>(q_norm), static_cast<const uint16_t*>(k_norm),
+                       static_cast<const uint16_t*>(cos_t), static_cast<const uint16_t*>(sin_t),
+                       static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache), eps};
+  return r4q::launch_flash_decode(qkv, qkv_stride, k_cache, v_cache, k_scale, v_scale, out, H * D,
+                                  B, H, Hk, max_seq, pos + 1, nullptr, nsplit, fwht,
+                                  static_cast<float*>(ctx->attn.ptr), r4q::as_stream(stream), &qk);
 }

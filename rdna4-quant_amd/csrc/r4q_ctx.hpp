@@ -17,6 +17,12 @@ struct DevBuf {
   void release();
 };
 
+// Number of DevBuf (re)allocations and releases so far in this process.  A
+// captured graph bakes in the addresses of the buffers it uses; its cache
+// key holds this count, so a graph is never replayed after any buffer could
+// have moved.
+uint64_t devbuf_epoch();
+
 struct GraphCache;  // captured decode steps (r4q_decode.hip)
 
 }  // namespace r4q

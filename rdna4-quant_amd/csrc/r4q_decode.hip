@@ -20,6 +20,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cstddef>
+#include <utility>
 #include <vector>
 
 #include "r4q_ctx.hpp"
@@ -30,12 +32,39 @@
 
 namespace r4q {
 
+// Captured graphs of a context, keyed by everything they bake in (model,
+// shape, buffer addresses); the least recently used one is dropped when the
+// cache is full.  All replay on one private stream.
 struct GraphCache {
+  static constexpr size_t kMax = 4;
+  struct Entry {
+    std::vector<uint8_t> key;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
   hipStream_t stream = nullptr;
-  hipGraphExec_t exec = nullptr;
-  std::vector<uint8_t> key;
+  std::vector<Entry> entries;
+  uint64_t clock = 0;
+  hipGraphExec_t find(const std::vector<uint8_t>& key) {
+    for (Entry& e : entries)
+      if (e.key == key) {
+        e.used = ++clock;
+        return e.exec;
+      }
+    return nullptr;
+  }
+  void insert(std::vector<uint8_t> key, hipGraphExec_t exec) {
+    if (entries.size() >= kMax) {
+      size_t lru = 0;
+      for (size_t i = 1; i < entries.size(); ++i)
+        if (entries[i].used < entries[lru].used) lru = i;
+      (void)hipGraphExecDestroy(entries[lru].exec);
+      entries.erase(entries.begin() + (std::ptrdiff_t)lru);
+    }
+    entries.push_back(Entry{std::move(key), exec, ++clock});
+  }
   ~GraphCache() {
-    if (exec) (void)hipGraphExecDestroy(exec);
+    for (Entry& e : entries) (void)hipGraphExecDestroy(e.exec);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -105,16 +134,9 @@ int validate(const r4q_model* m, int64_t B, Dims& dm) {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsplit, Bufs& bf) {
-  const size_t D = dm.D, I = dm.I;
-  const size_t lmN = m->final_norm ? (size_t)m->lm_N : 0;
-  const size_t rotw = dm.qd > dm.D ? dm.qd : dm.D;
-  const size_t sizes[] = {B * D, B * D, B * rotw, B * (size_t)dm.qkvN, B * D, B * 2 * I,
-                          B * I, B * D, B * lmN};
-  size_t total = 0;
-  for (size_t s : sizes) total += align256(s * 2);
-  // workspace of the batched projections (split-K partials): the largest
-  // any of the step's matrices asks for
+// Workspace of the batched projections (split-K partials): the largest any
+// of the step's matrices asks for (none at batch 1).
+size_t step_gemm_ws(const r4q_model* m, const Dims& dm, int64_t B) {
   size_t gws = 0;
   if (B > 1) {
     auto need = [&](int64_t N, int64_t K, int bits) {
@@ -129,6 +151,18 @@ int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsp
     }
     if (m->final_norm) need(m->lm_N, m->lm_K, m->lm_bits);
   }
+  return gws;
+}
+
+int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsplit, Bufs& bf) {
+  const size_t D = dm.D, I = dm.I;
+  const size_t lmN = m->final_norm ? (size_t)m->lm_N : 0;
+  const size_t rotw = dm.qd > dm.D ? dm.qd : dm.D;
+  const size_t sizes[] = {B * D, B * D, B * rotw, B * (size_t)dm.qkvN, B * D, B * 2 * I,
+                          B * I, B * D, B * lmN};
+  size_t total = 0;
+  for (size_t s : sizes) total += align256(s * 2);
+  const size_t gws = step_gemm_ws(m, dm, B);
   R4Q_TRY(ctx->step.reserve(total + gws));
   uint16_t** dst[] = {&bf.h, &bf.r, &bf.rot, &bf.qkv, &bf.o, &bf.gu, &bf.y, &bf.d, &bf.logits};
   uint8_t* p = static_cast<uint8_t*>(ctx->step.ptr);
@@ -408,22 +442,84 @@ int check_positions(const r4q_model* m, int64_t first, int64_t count) {
   return R4Q_OK;
 }
 
-// Key of a captured graph: model struct, layer table and launch shape.
-std::vector<uint8_t> graph_key(const r4q_model* m, int64_t B, int nsplit, const void* tokens_out,
-                               const Bufs& bf, const SampleCfg& scfg) {
-  std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 64 +
-                         sizeof(SampleCfg));
+// Key of a captured graph: model struct, layer table, launch shape and every
+// buffer address the graph bakes in (the context's buffers, the sampling
+// workspace, the caller's token array), plus the buffer epoch, which moves
+// whenever any context buffer is reallocated.
+std::vector<uint8_t> graph_key(int kind, const r4q_model* m, int64_t B, int nsplit,
+                               const void* tokens_out, const Bufs& bf, const SampleCfg& scfg,
+                               const void* sample_ws) {
+  const void* extra[] = {tokens_out, bf.h, bf.attn, bf.state, bf.ws, sample_ws};
+  const uint64_t epoch = devbuf_epoch();
+  std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 16 +
+                         sizeof(extra) + sizeof(epoch) + sizeof(SampleCfg));
   uint8_t* p = k.data();
   memcpy(p, m, sizeof(r4q_model));
   p += sizeof(r4q_model);
   memcpy(p, m->layers, sizeof(r4q_layer) * m->n_layers);
   p += sizeof(r4q_layer) * m->n_layers;
-  const void* extra[] = {tokens_out, bf.h, bf.attn, bf.state};
   memcpy(p, &B, 8);
   memcpy(p + 8, &nsplit, 4);
-  memcpy(p + 16, extra, sizeof(extra));
-  memcpy(p + 16 + sizeof(extra), &scfg, sizeof(SampleCfg));
+  memcpy(p + 12, &kind, 4);
+  p += 16;
+  memcpy(p, extra, sizeof(extra));
+  p += sizeof(extra);
+  memcpy(p, &epoch, sizeof(epoch));
+  p += sizeof(epoch);
+  memcpy(p, &scfg, sizeof(SampleCfg));
   return k;
+}
+
+enum GraphKind { kGraphLoop = 1, kGraphStep = 2 };
+
+// Runs a captured graph `reps` times on the context's graph stream, ordered
+// after the work already on `st` (and everything enqueued on `st` later waits
+// for it).  The device position state is first set to `pos`.  On a cache
+// miss `record(stream)` enqueues the work once under stream capture and the
+// instantiated graph is kept under `key`.
+template <class Record>
+int replay(r4q_ctx* ctx, hipStream_t st, std::vector<uint8_t> key, int* state, int pos,
+           int64_t reps, const Record& record) {
+  if (!ctx->graphs) ctx->graphs = new GraphCache();
+  GraphCache& gc = *ctx->graphs;
+  if (!gc.stream) R4Q_HIP_TRY(hipStreamCreateWithFlags(&gc.stream, hipStreamNonBlocking));
+  hipEvent_t ev;
+  R4Q_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  (void)hipEventRecord(ev, st);
+  (void)hipStreamWaitEvent(gc.stream, ev, 0);
+  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, gc.stream, state, pos);
+  int rc = launch_status("set_state");
+  hipGraphExec_t exec = rc == R4Q_OK ? gc.find(key) : nullptr;
+  if (rc == R4Q_OK && !exec) {
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamBeginCapture(gc.stream, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+      rc = fail(R4Q_EHIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    } else {
+      const int rc1 = record(gc.stream);
+      e = hipStreamEndCapture(gc.stream, &graph);
+      if (rc1 != R4Q_OK) rc = rc1;
+      else if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+      else {
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+          exec = nullptr;
+          rc = fail(R4Q_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+        } else {
+          gc.insert(std::move(key), exec);
+        }
+      }
+      if (graph) (void)hipGraphDestroy(graph);
+    }
+  }
+  for (int64_t t = 0; rc == R4Q_OK && t < reps; ++t) {
+    const hipError_t e = hipGraphLaunch(exec, gc.stream);
+    if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+  }
+  (void)hipEventRecord(ev, gc.stream);
+  (void)hipStreamWaitEvent(st, ev, 0);
+  (void)hipEventDestroy(ev);
+  return rc;
 }
 
 }  // namespace
@@ -431,8 +527,27 @@ std::vector<uint8_t> graph_key(const r4q_model* m, int64_t B, int nsplit, const 
 
 using namespace r4q;
 
-extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
-                               int64_t pos, void* hidden_out, void* logits, void* stream) {
+extern "C" int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int64_t n) {
+  using namespace r4q;
+  R4Q_REQUIRE(out && n >= 2, "decode_plan: need room for 2 values");
+  Dims dm;
+  R4Q_TRY(validate(m, B, dm));
+  const size_t gws = step_gemm_ws(m, dm, B);
+  int fused = 0;
+  for (int li = 0; li < dm.L; ++li) {
+    const int bits = m->layers[li].gu_bits;
+    fused += B == 1 ? (bits != 16 && gemv_silu_ok(2 * (int64_t)dm.I, dm.D, bits))
+                    : gemm_skinny_silu_ok(B, dm.I, dm.D, bits, gws);
+  }
+  out[0] = attn_num_splits(m->max_seq, B, dm.Hk);
+  out[1] = fused;
+  return R4Q_OK;
+}
+
+namespace r4q {
+namespace {
+int decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B, int64_t pos,
+                void* hidden_out, void* logits, bool use_graph, void* stream) {
   R4Q_REQUIRE(ctx && hidden_in, "decode_step: null context or input");
   Dims dm;
   R4Q_TRY(validate(m, B, dm));
@@ -443,13 +558,41 @@ extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hid
   R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
   R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
-  R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, logits != nullptr, st));
+  const bool want_logits = logits != nullptr;
+  if (use_graph) {
+    // the same step with the position read from device memory; one graph
+    // serves every position (the attention split count depends only on the
+    // cache capacity)
+    auto record = [&](hipStream_t gs) {
+      return enqueue_step(m, dm, B, pos, bf.state + kPos, bf.state + kSeq, nsplit, bf,
+                          want_logits, gs);
+    };
+    R4Q_TRY(replay(ctx, st,
+                   graph_key(want_logits ? kGraphStep : -kGraphStep, m, B, nsplit, nullptr, bf,
+                             SampleCfg{0.f, 1.f, 0}, nullptr),
+                   bf.state, (int)pos, 1, record));
+  } else {
+    R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, want_logits, st));
+  }
   if (logits)
     R4Q_HIP_TRY(hipMemcpyAsync(logits, bf.logits, (size_t)B * m->lm_N * 2,
                                hipMemcpyDeviceToDevice, st));
   if (hidden_out)
     R4Q_HIP_TRY(hipMemcpyAsync(hidden_out, bf.h, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
   return R4Q_OK;
+}
+}  // namespace
+}  // namespace r4q
+
+extern "C" int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t B,
+                               int64_t pos, void* hidden_out, void* logits, void* stream) {
+  return r4q::decode_step(ctx, m, hidden_in, B, pos, hidden_out, logits, false, stream);
+}
+
+extern "C" int r4q_decode_step_graph(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
+                                     int64_t B, int64_t pos, void* hidden_out, void* logits,
+                                     void* stream) {
+  return r4q::decode_step(ctx, m, hidden_in, B, pos, hidden_out, logits, true, stream);
 }
 
 namespace r4q {
@@ -483,54 +626,15 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
     }
     return R4Q_OK;
   }
-  // ---- graph path
-  if (!ctx->graphs) ctx->graphs = new GraphCache();
-  GraphCache& gc = *ctx->graphs;
-  if (!gc.stream) R4Q_HIP_TRY(hipStreamCreateWithFlags(&gc.stream, hipStreamNonBlocking));
-  hipEvent_t ev;
-  R4Q_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-  (void)hipEventRecord(ev, st);
-  (void)hipStreamWaitEvent(gc.stream, ev, 0);
-  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, gc.stream, bf.state, (int)start_pos);
-  int rc = launch_status("set_state");
-  std::vector<uint8_t> key = graph_key(m, B, nsplit, tokens_out, bf, scfg);
-  if (rc == R4Q_OK && (!gc.exec || gc.key != key)) {
-    if (gc.exec) {
-      (void)hipGraphExecDestroy(gc.exec);
-      gc.exec = nullptr;
-    }
-    hipGraph_t graph = nullptr;
-    hipError_t e = hipStreamBeginCapture(gc.stream, hipStreamCaptureModeRelaxed);
-    if (e != hipSuccess) {
-      rc = fail(R4Q_EHIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
-    } else {
-      const int* pos_dev = bf.state + kPos;
-      const int* seq_dev = bf.state + kSeq;
-      int rc1 = enqueue_step(m, dm, B, start_pos, pos_dev, seq_dev, nsplit, bf, true, gc.stream);
-      if (rc1 == R4Q_OK) rc1 = enqueue_sample(m, dm, B, bf, toks, true, 0, gc.stream, &scfg, sws);
-      e = hipStreamEndCapture(gc.stream, &graph);
-      if (rc1 != R4Q_OK) rc = rc1;
-      else if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
-      else {
-        e = hipGraphInstantiate(&gc.exec, graph, nullptr, nullptr, 0);
-        if (e != hipSuccess) {
-          gc.exec = nullptr;
-          rc = fail(R4Q_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-        } else {
-          gc.key = key;
-        }
-      }
-      if (graph) (void)hipGraphDestroy(graph);
-    }
-  }
-  for (int64_t t = 0; rc == R4Q_OK && t < num_tokens; ++t) {
-    const hipError_t e = hipGraphLaunch(gc.exec, gc.stream);
-    if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipGraphLaunch: %s", hipGetErrorString(e));
-  }
-  (void)hipEventRecord(ev, gc.stream);
-  (void)hipStreamWaitEvent(st, ev, 0);
-  (void)hipEventDestroy(ev);
-  return rc;
+  // ---- graph path: one captured step + next-token choice + position
+  // advance, replayed num_tokens times
+  auto record = [&](hipStream_t gs) {
+    R4Q_TRY(enqueue_step(m, dm, B, start_pos, bf.state + kPos, bf.state + kSeq, nsplit, bf, true,
+                         gs));
+    return enqueue_sample(m, dm, B, bf, toks, true, 0, gs, &scfg, sws);
+  };
+  return replay(ctx, st, graph_key(kGraphLoop, m, B, nsplit, tokens_out, bf, scfg, sws),
+                bf.state, (int)start_pos, num_tokens, record);
 }
 }  // namespace
 }  // namespace r4q

@@ -737,7 +737,7 @@ int skinny_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
     const int64_t c = (ntiles * se + kCUs - 1) / kCUs * kps + se;
     if (c <= best) best = c, S = se;
   }
-  if (const char* e = getenv("R4Q_SKINNY_SPLITS")) S = atoi(e);  // tuning override
+  if (const int v = tuning().skinny_splits.load()) S = v;  // measurement override (r4q_tune)
   if (S < 2) return 1;
   // every split non-empty
   const int64_t kps = (kt + S - 1) / S;
@@ -860,8 +860,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
     consider(0, S);
     if (tiles > 256 && tiles % 256) consider(tiles - tiles % 256, S);
   }
-  if (const char* e = getenv("R4Q_GEMM_SPLITS")) {  // tuning override: every tile split
-    const int v = atoi(e);
+  if (const int v = tuning().gemm_splits.load()) {  // measurement override: every tile split
     const size_t ws = (size_t)v * tiles * RBM * RBN * 4;
     if (v >= 2 && v <= kMaxGemmSplits && nk / v >= 1 && ws <= ws_bytes) {
       best.full = 0;

@@ -602,12 +602,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   }
 }
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  if (!v || !*v) return dflt;
-  return atoi(v);
-}
-
 template <int WBITS>
 int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64_t N, int64_t K,
                     const GemvNorm* norm, int xm, int epi, hipStream_t st) {
@@ -622,7 +616,7 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   // or at <= kCpl when 256 lanes cannot
   int lpr = 16;
   while (lpr < 256 && lpr * 5 < cpr) lpr *= 2;
-  lpr = env_int("R4Q_GEMV_LPR", lpr);
+  if (const int v = tuning().gemv_lpr.load()) lpr = v;  // measurement override (r4q_tune)
   R4Q_REQUIRE(lpr * kCpl >= cpr, "gemv: K=%lld needs more than 256 lanes per row", (long long)K);
   const int rps = 256 / lpr;
   if (epi != kEpiRows)
@@ -646,8 +640,9 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   const bool nrm = xm == kXNorm;
   const int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : 256)
                        : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
-  const int max_wg = env_int("R4Q_GEMV_WGS", dflt);
-  const int ub = env_int("R4Q_GEMV_UB", 1);
+  const int wgs_o = tuning().gemv_wgs.load(), ub_o = tuning().gemv_ub.load();
+  const int max_wg = wgs_o ? wgs_o : dflt;
+  const int ub = ub_o ? ub_o : 1;
   const int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
   const int64_t grid = (nsteps + per - 1) / per;
   // the staging area also holds one partial per (step, wave) of the workgroup

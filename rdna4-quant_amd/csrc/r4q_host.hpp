@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/r4q.h"
 
 namespace r4q {
@@ -17,6 +19,22 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 // Converts the pending launch status (hipGetLastError) into a return code.
 int launch_status(const char* what);
+
+// Launch-shape overrides for measurement sweeps; 0 = the built-in choice.
+// Initial values come from the environment, read once per process (first
+// use) and validated there; r4q_tune() changes them later.  A value outside
+// its range is ignored (environment) or rejected (r4q_tune).
+//   gemv_lpr      R4Q_GEMV_LPR      lanes per GEMV row: 16, 32, 64, 128, 256
+//   gemv_wgs      R4Q_GEMV_WGS      GEMV workgroup cap: 1 .. 65536
+//   gemv_ub       R4Q_GEMV_UB       GEMV steps per batch: 1 or 2
+//   attn_splits   R4Q_ATTN_SPLITS   flash-decode splits: 1 .. 128
+//   skinny_splits R4Q_SKINNY_SPLITS skinny-GEMM K splits: 1 .. 8
+//   gemm_splits   R4Q_GEMM_SPLITS   ring-GEMM K splits of every tile: 1 .. 16
+struct Tuning {
+  std::atomic<int> gemv_lpr{0}, gemv_wgs{0}, gemv_ub{0};
+  std::atomic<int> attn_splits{0}, skinny_splits{0}, gemm_splits{0};
+};
+Tuning& tuning();
 
 }  // namespace r4q
 

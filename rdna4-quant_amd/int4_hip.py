@@ -21,7 +21,8 @@ device work, unlike the reference which does not check.
 from __future__ import annotations
 
 import ctypes as C
-from typing import List, Sequence
+import weakref
+from typing import List
 
 import torch
 
@@ -178,12 +179,17 @@ def dbg_rope(Q, K, COS, SIN, H: int, Hk: int, D: int) -> List[torch.Tensor]:
 # ------------------------------------------------------------ decode family
 class _Model:
     """A C `r4q_model` built from the reference's per-layer tensor lists.
-    Holds references to every tensor it points at."""
 
-    def __init__(self, keep, struct, layers):
-        self.keep = keep
+    It holds no strong reference to the caller's tensors (the cache would
+    otherwise keep every model ever passed alive, ~11 GB at Qwen3-14B per
+    reload): each tensor it points at carries a weak reference whose callback
+    drops the cache entry when the tensor is freed, before its memory or its
+    id() can be reused."""
+
+    def __init__(self, struct, layers):
         self.struct = struct
         self.layers = layers
+        self.refs = []
 
 
 _models = {}
@@ -200,16 +206,34 @@ def _context():
 
 
 def _key_of(objs):
+    """Cache key of an argument block: tensors by identity (their lists as
+    tuples of ids), everything else by value.  A hit is valid because every
+    tensor of a cached model is alive (see _Model)."""
     key = []
     for o in objs:
-        if isinstance(o, torch.Tensor):
-            key.append((o.data_ptr(), tuple(o.shape), o.dtype))
-        elif isinstance(o, (list, tuple)):
-            key.append(tuple((t.data_ptr(), tuple(t.shape), t.dtype) if isinstance(t, torch.Tensor)
-                             else t for t in o))
+        if isinstance(o, (list, tuple)):
+            # tensor lists (None entries allowed) by identity, int lists by value
+            key.append(tuple(map(id, o)) if o and isinstance(o[0], torch.Tensor) else tuple(o))
+        elif isinstance(o, torch.Tensor):
+            key.append(id(o))
         else:
             key.append(o)
     return tuple(key)
+
+
+def _forget(key):
+    def cb(_ref):
+        _models.pop(key, None)
+    return cb
+
+
+def _watch(m, key, objs):
+    cb = _forget(key)
+    for o in objs:
+        if isinstance(o, torch.Tensor):
+            m.refs.append(weakref.ref(o, cb))
+        elif isinstance(o, (list, tuple)):
+            m.refs.extend(weakref.ref(t, cb) for t in o if isinstance(t, torch.Tensor))
 
 
 def build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N,
@@ -218,12 +242,13 @@ def build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, do
                 k_caches, v_caches, final_norm_w=None, lm_w=None, lm_s=None, lm_N=0, lm_K=0,
                 embed_weight=None, kv_scales=None) -> _Model:
     """Validates the reference argument block and returns a cached model
-    descriptor (keyed by tensor addresses and shapes)."""
+    descriptor (keyed by tensor identity; see _key_of / _Model)."""
     args = [qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N,
             in_norm_w, post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, num_heads,
             num_kv_heads, head_dim, hidden_size, intermediate_size, float(rms_eps), k_caches,
             v_caches, final_norm_w, lm_w, lm_s, lm_N, lm_K, embed_weight,
-            None if kv_scales is None else (tuple(kv_scales[0]), tuple(kv_scales[1]))]
+            None if kv_scales is None else kv_scales[0],
+            None if kv_scales is None else kv_scales[1]]
     key = _key_of(args)
     m = _models.get(key)
     if m is not None:
@@ -242,7 +267,6 @@ def build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, do
           "KV caches must be uint8 [B, Hk, max_seq, head_dim]")
     max_seq = k_caches[0].shape[2]
     layers = (_R.R4QLayer * L)()
-    keep = []
     for li in range(L):
         ly = layers[li]
         specs = (("qkv", qkv_w[li], qkv_s[li], qkv_N[li], D), ("o", o_w[li], o_s[li], o_N[li], H * hd),
@@ -274,8 +298,6 @@ def build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, do
             _need(vs.dtype == torch.float32 and vs.numel() == Hk, "v scale must be float32 [Hk]")
             ly.k_scale = ks.data_ptr()
             ly.v_scale = vs.data_ptr()
-            keep += [ks, vs]
-    keep += list(args[:18]) + [k_caches, v_caches]
     st = _R.R4QModel()
     st.n_layers, st.n_heads, st.n_kv_heads, st.head_dim = L, H, Hk, hd
     st.hidden, st.inter, st.eps = D, I, float(rms_eps)
@@ -292,13 +314,12 @@ def build_model(qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, do
         st.lm_w = lm_w.data_ptr()
         st.lm_s = None if bits == 16 else lm_s.data_ptr()
         st.lm_N, st.lm_K, st.lm_bits = lm_N, lm_K, bits
-        keep += [final_norm_w, lm_w, lm_s]
     if embed_weight is not None:
         _cuda_half(embed_weight, "embed_weight")
         st.embed = embed_weight.data_ptr()
         st.vocab = embed_weight.shape[0]
-        keep.append(embed_weight)
-    m = _Model(keep, st, layers)
+    m = _Model(st, layers)
+    _watch(m, key, args)
     _models[key] = m
     return m
 
@@ -320,19 +341,28 @@ def _decode_common(hidden_in, layer_args, k_caches, v_caches, final=None, embed=
     return m, B, int(pos)
 
 
+def _step_entry(use_graph):
+    """The C entry point of one decode step: the graph-replayed step unless
+    the caller is capturing torch's stream itself (or asks for eager)."""
+    if use_graph is None:
+        use_graph = not torch.cuda.is_current_stream_capturing()
+    return "r4q_decode_step_graph" if use_graph else "r4q_decode_step"
+
+
 def decode_step(hidden_in, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s,
                 down_N, in_norm_w, post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, pos,
                 num_heads, num_kv_heads, head_dim, hidden_size, intermediate_size, rms_eps,
-                k_caches, v_caches, hadamard_mat, *, kv_scales=None):
+                k_caches, v_caches, hadamard_mat, *, kv_scales=None, use_graph=None):
     """All layers for one token; returns the final hidden state [B, 1, D]
     (hip:2343-2528).  `hadamard_mat` is accepted and unused, as in the
-    reference's live kernels."""
+    reference's live kernels.  The step is replayed from a captured hipGraph
+    (bit-identical to the eager launches; use_graph=False forces those)."""
     la = (qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N, in_norm_w,
           post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, pos, num_heads, num_kv_heads,
           head_dim, hidden_size, intermediate_size, rms_eps)
     m, B, pos = _decode_common(hidden_in, la, k_caches, v_caches, kv_scales=kv_scales)
     out = torch.empty((B, 1, hidden_size), dtype=torch.float16, device=hidden_in.device)
-    _R.call("r4q_decode_step", _context(), C.byref(m.struct), hidden_in.data_ptr(), B, pos,
+    _R.call(_step_entry(use_graph), _context(), C.byref(m.struct), hidden_in.data_ptr(), B, pos,
             out.data_ptr(), None, _stream())
     return out
 
@@ -341,17 +371,20 @@ def decode_step_logits(hidden_in, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s
                        down_s, down_N, in_norm_w, post_norm_w, q_norm_w, k_norm_w, rope_cos,
                        rope_sin, pos, num_heads, num_kv_heads, head_dim, hidden_size,
                        intermediate_size, rms_eps, k_caches, v_caches, final_norm_w, lm_w, lm_s,
-                       lm_N, lm_K, hadamard_mat, *, kv_scales=None):
+                       lm_N, lm_K, hadamard_mat, *, kv_scales=None, use_graph=None):
     """All layers + final norm + LM head; returns logits [B, 1, lm_N] fp16
-    (hip:2534-2595)."""
+    (hip:2534-2595).  The engine calls this once per token
+    (int4_engine_v5.py:272); the step is replayed from a captured hipGraph
+    with the position set on the device (bit-identical to the eager launches;
+    use_graph=False forces those)."""
     la = (qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s, down_N, in_norm_w,
           post_norm_w, q_norm_w, k_norm_w, rope_cos, rope_sin, pos, num_heads, num_kv_heads,
           head_dim, hidden_size, intermediate_size, rms_eps)
     m, B, pos = _decode_common(hidden_in, la, k_caches, v_caches,
                                final=(final_norm_w, lm_w, lm_s, lm_N, lm_K), kv_scales=kv_scales)
     logits = torch.empty((B, 1, lm_N), dtype=torch.float16, device=hidden_in.device)
-    _R.call("r4q_decode_step", _context(), C.byref(m.struct), hidden_in.data_ptr(), B, pos, None,
-            logits.data_ptr(), _stream())
+    _R.call(_step_entry(use_graph), _context(), C.byref(m.struct), hidden_in.data_ptr(), B, pos,
+            None, logits.data_ptr(), _stream())
     return logits
 
 

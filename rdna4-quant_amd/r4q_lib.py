@@ -76,6 +76,7 @@ SIGNATURES = {
     "r4q_res_rmsnorm_fwht": [_p, _p, _p, _p, _p, _i64, _i64, _f32, _p],
     "r4q_fwht32": [_p, _p, _i64, _p],
     "r4q_hbm_read": [_p, _i64, _p, _i64, _p],
+    "r4q_tune": [C.c_char_p, C.c_int],
     "r4q_silu_mul_fwht": [_p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_silu_mul": [_p, _p, _p, _i64, _i64, _i64, _i64, _p],
     "r4q_head_rmsnorm": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _p],
@@ -91,7 +92,11 @@ SIGNATURES = {
     "r4q_ctx_destroy": [_p],
     "r4q_flash_decode": [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                          _i64, C.c_int, _p],
+    "r4q_flash_decode_qkv": [_p, _p, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p, _i64,
+                             _i64, _i64, _i64, _i64, _i64, _i64, C.c_int, _p],
     "r4q_decode_step": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _p, _p, _p],
+    "r4q_decode_plan": [C.POINTER(R4QModel), _i64, C.POINTER(_i32), _i64],
+    "r4q_decode_step_graph": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _p, _p, _p],
     "r4q_decode_bench": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _i64, C.c_int, _p, _p],
     "r4q_decode_generate": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _i64, C.c_int, _f32, _f32,
                             C.c_uint64, _p, _p],
@@ -142,6 +147,11 @@ def check(rc: int, what: str = "") -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args), name)
+
+
+def tune(name: str, value: int) -> None:
+    """Process-wide launch-shape override (r4q_tune); 0 restores the default."""
+    call("r4q_tune", name.encode(), int(value))
 
 
 def ptr(t) -> int | None:

@@ -94,10 +94,12 @@ def norm_weight(D: int, g: torch.Generator, device="cpu") -> torch.Tensor:
 
 
 def rope_tables(head_dim: int, max_pos: int, theta: float = 1.0e6, device="cpu"):
-    """fp16 cos/sin [max_pos, head_dim/2] (engine_utils.py:70-76 convention),
-    computed in float64."""
-    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
-    ang = torch.outer(torch.arange(max_pos, dtype=torch.float64), inv)
+    """fp16 cos/sin [max_pos, head_dim/2] built as precompute_rope_freqs does
+    (engine_utils.py:70-76): float32 frequencies, positions and angles, cos and
+    sin in float32, then fp16 (on the CPU, so the tables do not depend on the
+    device)."""
+    freqs = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    ang = torch.outer(torch.arange(max_pos).float(), freqs)
     return ang.cos().half().to(device).contiguous(), ang.sin().half().to(device).contiguous()
 
 
@@ -137,3 +139,63 @@ def random_kv_values(Hk: int, n_fill: int, hd: int, g: torch.Generator, device="
     an FP8 KV cache (by the library's fp16_to_fp8 on the device, or by the
     oracle in CPU tests)."""
     return (torch.randn(batch, Hk, n_fill, hd, generator=g, device=device) * scale).half()
+
+
+def qwen3_model(ctx: int, extra: int, batch: int, device, log=None) -> dict:
+    """The BASELINE config-4 model, generated on `device`: 40 Qwen3-14B-shaped
+    layers (seed 4; 32 of the 160 projection matrices INT8 by
+    precision_mask), FP16 embedding and LM head, FP8 KV caches of capacity
+    ctx + extra per layer with positions [0, ctx) holding the reference
+    encoder's codes of N(0,1) values (the library's fp16_to_fp8).  Returns a
+    dict with the int4_hip argument lists ("args"), caches ("kc", "vc"), RoPE
+    tables, final norm, LM head, embedding, dims and byte counts."""
+    import int4_hip
+
+    c = QWEN3_14B
+    D, I, H, Hk, hd, L, V = c["hidden"], c["inter"], c["heads"], c["kv_heads"], c["head_dim"], \
+        c["layers"], c["vocab"]
+    g = gen(4, device)
+    mask = precision_mask(L, seed=4)
+    args = {k: [] for k in ("qkv_w", "qkv_s", "qkv_N", "o_w", "o_s", "o_N", "gu_w", "gu_s", "gu_N",
+                            "down_w", "down_s", "down_N", "in_norm", "post_norm", "q_norm",
+                            "k_norm")}
+    wbytes = 0
+    for li in range(L):
+        bits = {n: mask[(li, n)] for n in ("qkv", "o", "gu", "down")}
+        ly = make_layer(D, I, H, Hk, hd, g, device=device, bits=bits)
+        for k in args:
+            args[k].append(ly[k])
+        for n in ("qkv", "o", "gu", "down"):
+            N = ly[n + "_N"]
+            K = {"qkv": D, "o": H * hd, "gu": D, "down": I}[n]
+            wbytes += N * K * ly[n + "_bits"] // 8 + N * (K // 32) * 3
+        if log and (li + 1) % 10 == 0:
+            log(f"layer {li + 1}/{L} generated")
+    max_seq = ctx + extra
+    kc, vc = [], []
+    for li in range(L):
+        k = torch.zeros(batch, Hk, max_seq, hd, dtype=torch.uint8, device=device)
+        v = torch.zeros_like(k)
+        k[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
+        v[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
+        kc.append(k)
+        vc.append(v)
+    cos, sin = rope_tables(hd, max_seq, c["rope_theta"], device)
+    final_norm = norm_weight(D, g, device)
+    lm_w, _ = fp16_weight(V, D, g, device)
+    embed, _ = fp16_weight(V, D, g, device)
+    return dict(args=args, kc=kc, vc=vc, cos=cos, sin=sin, final_norm=final_norm, lm_w=lm_w,
+                embed=embed, D=D, I=I, H=H, Hk=Hk, hd=hd, L=L, V=V, eps=c["eps"], mask=mask,
+                max_seq=max_seq, wbytes=wbytes, lm_bytes=V * D * 2)
+
+
+def qwen3_bench_args(m: dict, start_pos: int) -> tuple:
+    """int4_hip decode_bench / decode_loop argument tail of a qwen3_model
+    (layer block at start_pos, caches, final norm, LM head, hadamard)."""
+    a = m["args"]
+    had = torch.zeros(32, 32, dtype=torch.float16, device=m["lm_w"].device)
+    return (a["qkv_w"], a["qkv_s"], a["qkv_N"], a["o_w"], a["o_s"], a["o_N"], a["gu_w"],
+            a["gu_s"], a["gu_N"], a["down_w"], a["down_s"], a["down_N"], a["in_norm"],
+            a["post_norm"], a["q_norm"], a["k_norm"], m["cos"], m["sin"], start_pos, m["H"],
+            m["Hk"], m["hd"], m["D"], m["I"], m["eps"], m["kc"], m["vc"], m["final_norm"],
+            m["lm_w"], None, m["V"], m["D"], had)

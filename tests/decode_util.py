@@ -142,3 +142,42 @@ def oracle_step(m, hidden16, pos, kc, vc, b=0, forced_kv=None, kv_trace=None):
                          lm_s=None if m.lm_s is None else m.lm_s.numpy().reshape(m.vocab, -1, 2),
                          lm_bits=m.lm_bits, k_scales=ks, v_scales=vs, forced_kv=forced_kv,
                          kv_trace=kv_trace)
+
+
+def plan(m, B):
+    """r4q_decode_plan of the model: (attention split count, layers whose
+    gate/up applies the SiLU gate in the same launch)."""
+    import ctypes as C
+
+    import r4q_lib as R
+    had = torch.zeros(32, 32, dtype=torch.float16, device=m.dev)
+    args = layer_args(m, 0)
+    md = int4_hip.build_model(*args[:18], *args[19:], m.k_caches, m.v_caches, m.final_norm_d,
+                              m.lm_w_d, m.lm_s_d, m.vocab, m.D)
+    del had
+    out = (C.c_int32 * 2)()
+    R.call("r4q_decode_plan", C.byref(md.struct), B, out, 2)
+    return int(out[0]), int(out[1])
+
+
+def oracle_batch_forced(m, h, pos):
+    """Batched oracle step for every row with the GPU's KV codes at `pos`
+    (each differing code checked to be explainable by last-bit rounding);
+    returns (hidden [B, D], logits [B, V], number of differing codes, total)."""
+    B = m.batch
+    kc = [m.kc_np[li].copy() for li in range(m.L)]
+    vc = [m.vc_np[li].copy() for li in range(m.L)]
+    forced = [(m.k_caches[li][:, :, pos].cpu().numpy(), m.v_caches[li][:, :, pos].cpu().numpy())
+              for li in range(m.L)]
+    trace = []
+    ks = None if m.k_scales is None else [t.numpy() for t in m.k_scales]
+    vs = None if m.v_scales is None else [t.numpy() for t in m.v_scales]
+    hid, logits = O.decode_step_batch(
+        m.oracle_layers, h.reshape(B, -1), pos, kc, vc, H=m.H, Hk=m.Hk, D=m.hd, hidden=m.D,
+        inter=m.I, eps=m.eps, rope_cos=m.cos.numpy(), rope_sin=m.sin.numpy(),
+        final_norm=m.final_norm.numpy(), lm_w=m.lm_w.numpy(),
+        lm_s=None if m.lm_s is None else m.lm_s.numpy().reshape(m.vocab, -1, 2),
+        lm_bits=m.lm_bits, k_scales=ks, v_scales=vs, forced_kv=forced, kv_trace=trace)
+    n = check_forced_kv(forced, trace)
+    total = sum(k.size + v.size for k, v in forced)
+    return hid, logits, n, total

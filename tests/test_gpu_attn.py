@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 import torch
 
+import int4_hip
 import r4q_lib as R
 import r4q_oracle as O
 import r4q_synth as S
@@ -65,13 +66,16 @@ def test_flash_decode_batch8_no_rotation(dev, ctx):
 
 
 @pytest.mark.parametrize("L", [257, 8192])
-def test_flash_decode_forced_split_counts(dev, ctx, monkeypatch, L):
+def test_flash_decode_forced_split_counts(dev, ctx, L):
     """Split counts from 1 to 128 back to back on one context: more than one
     64-split merge round, and splits that hold no positions when there are
     fewer 32-position chunks than splits."""
-    for n in (3, 100, 1, 17, 128, 64, 2):
-        monkeypatch.setenv("R4Q_ATTN_SPLITS", str(n))
-        _case(dev, ctx, 2, 40, 8, L, L + 1, scaled=True, fwht=True, seed=n + L)
+    try:
+        for n in (3, 100, 1, 17, 128, 64, 2):
+            R.tune("attn_splits", n)
+            _case(dev, ctx, 2, 40, 8, L, L + 1, scaled=True, fwht=True, seed=n + L)
+    finally:
+        R.tune("attn_splits", 0)
 
 
 def test_flash_decode_single_position_is_v(dev, ctx):
@@ -115,3 +119,106 @@ def test_flash_decode_rejects_bad_arguments(dev, ctx):
     rc = R.lib().r4q_flash_decode(ctx, z.data_ptr(), 5120, z.data_ptr(), z.data_ptr(), None, None,
                                   z.data_ptr(), 1, 42, 8, 128, 16, 4, 1, None)
     assert rc == R.R4Q_EINVAL
+
+
+@pytest.mark.parametrize("B", [1, 8])
+@pytest.mark.parametrize("pos", [0, 2047, 32767])
+@pytest.mark.parametrize("scaled", [False, True])
+def test_fused_prologue_kv_bytes_and_output_bit_exact(dev, ctx, B, pos, scaled):
+    """The decode step's attention prologue (r4q_flash_decode_qkv: head norm +
+    RoPE of raw QKV rows, FP8 K/V write at pos, attention over 0..pos) against
+    the two-kernel route (r4q_head_norm_rope_kv, then r4q_flash_decode on its
+    q rows and caches) and the oracle:
+      * the K/V codes written at pos are bit-identical to the standalone
+        kernel's and to the oracle's (K encoded from the fp32 rotated value,
+        hip:1667-1675), and no other cache byte changes;
+      * with the same split count the attention outputs are bit-identical;
+      * with the decode step's own split count (from the cache capacity) the
+        output matches the float64 oracle (rel-L2 <= 5e-3)."""
+    H, Hk, D = 40, 8, 128
+    qkvN = (H + 2 * Hk) * D
+    max_seq = pos + 34
+    print(f"[prologue] B={B} pos={pos} scaled={scaled}", flush=True)
+    g = S.gen(1000 + pos + B + 7 * scaled)
+    qkv = (torch.randn(B, qkvN, generator=g) * 2).half()
+    qw, kw = S.norm_weight(D, g), S.norm_weight(D, g)
+    cos, sin = S.rope_tables(D, max_seq)
+    ks = (0.25 + torch.rand(Hk, generator=g)).float() if scaled else None
+    vs = (0.25 + torch.rand(Hk, generator=g)).float() if scaled else None
+    QKV, QW, KW, COS, SIN = (t.to(dev) for t in (qkv, qw, kw, cos, sin))
+    Ks, Vs = (ks.to(dev), vs.to(dev)) if scaled else (None, None)
+    # caches: FP8 codes of N(0,1) values (the reference encoder, on the GPU) below pos
+    gd = torch.Generator(device=dev)
+    gd.manual_seed(pos + B)
+    kc0 = torch.zeros(B, Hk, max_seq, D, dtype=torch.uint8, device=dev)
+    vc0 = torch.zeros_like(kc0)
+    if pos:
+        for c in (kc0, vc0):
+            vals = torch.randn(B, Hk, pos, D, device=dev, generator=gd).half()
+            c[:, :, :pos] = int4_hip.fp16_to_fp8(vals)
+            del vals
+    kc1, vc1, kc2, vc2 = kc0.clone(), vc0.clone(), kc0.clone(), vc0.clone()
+    out1 = torch.empty(B, H * D, dtype=torch.float16, device=dev)
+    out2 = torch.empty_like(out1)
+    qo = torch.empty(B, (H + Hk) * D, dtype=torch.float16, device=dev)
+    nsp = min(32, max(1, (max_seq + 127) // 128))
+    try:
+        R.tune("attn_splits", nsp)
+        R.call("r4q_flash_decode_qkv", ctx, QKV.data_ptr(), qkvN, QW.data_ptr(), KW.data_ptr(),
+               COS.data_ptr(), SIN.data_ptr(), C.c_float(1e-6), kc1.data_ptr(), vc1.data_ptr(),
+               R.ptr(Ks), R.ptr(Vs), out1.data_ptr(), B, H, Hk, D, max_seq, max_seq, pos, 1,
+               R.stream_handle())
+        R.call("r4q_head_norm_rope_kv", QKV.data_ptr(), qkvN, QW.data_ptr(), KW.data_ptr(),
+               qo.data_ptr(), (H + Hk) * D, kc2.data_ptr(), vc2.data_ptr(), R.ptr(Ks), R.ptr(Vs),
+               COS.data_ptr(), SIN.data_ptr(), B, H, Hk, D, C.c_float(1e-6), max_seq, pos,
+               R.stream_handle())
+        R.call("r4q_flash_decode", ctx, qo.data_ptr(), (H + Hk) * D, kc2.data_ptr(),
+               vc2.data_ptr(), R.ptr(Ks), R.ptr(Vs), out2.data_ptr(), B, H, Hk, D, max_seq,
+               pos + 1, 1, R.stream_handle())
+    finally:
+        R.tune("attn_splits", 0)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(out1, out2)
+    # only position pos changed
+    for c1, c0 in ((kc1, kc0), (vc1, vc0)):
+        assert torch.equal(c1[:, :, :pos], c0[:, :, :pos])
+        assert torch.equal(c1[:, :, pos + 1:], c0[:, :, pos + 1:])
+    # the decode step's own split count, then the oracle
+    out3 = torch.empty_like(out1)
+    R.call("r4q_flash_decode_qkv", ctx, QKV.data_ptr(), qkvN, QW.data_ptr(), KW.data_ptr(),
+           COS.data_ptr(), SIN.data_ptr(), C.c_float(1e-6), kc1.data_ptr(), vc1.data_ptr(),
+           R.ptr(Ks), R.ptr(Vs), out3.data_ptr(), B, H, Hk, D, max_seq, max_seq, pos, 1,
+           R.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    for b in sorted({0, B - 1}):
+        q_out, _, kb, vb = O.head_norm_rope_kv(
+            qkv[b].numpy(), qw.numpy(), kw.numpy(), cos.numpy(), sin.numpy(), pos, H, Hk, D,
+            1e-6, None if ks is None else ks.numpy(), None if vs is None else vs.numpy())
+        assert np.array_equal(kc1[b, :, pos].cpu().numpy(), kb), b
+        assert np.array_equal(vc1[b, :, pos].cpu().numpy(), vb), b
+        kcb, vcb = kc1[b].cpu().numpy(), vc1[b].cpu().numpy()
+        want = O.attention_decode(q_out, kcb, vcb, pos + 1, H, Hk, D,
+                                  None if ks is None else ks.numpy(),
+                                  None if vs is None else vs.numpy(), fwht=True)
+        assert rel_l2(out3[b].cpu().numpy(), want) <= TOL, (b, rel_l2(out3[b].cpu().numpy(), want))
+    # the other rows' codes too (cheap: no attention)
+    for b in range(B):
+        _, _, kb, vb = O.head_norm_rope_kv(
+            qkv[b].numpy(), qw.numpy(), kw.numpy(), cos.numpy(), sin.numpy(), pos, H, Hk, D,
+            1e-6, None if ks is None else ks.numpy(), None if vs is None else vs.numpy())
+        assert np.array_equal(kc1[b, :, pos].cpu().numpy(), kb), b
+        assert np.array_equal(vc1[b, :, pos].cpu().numpy(), vb), b
+
+
+def test_fused_prologue_rejects_bad_arguments(dev, ctx):
+    z = torch.zeros(7168, dtype=torch.float16, device=dev)
+    c8 = torch.zeros(8 * 16 * 128, dtype=torch.uint8, device=dev)
+    args = [ctx, z.data_ptr(), 7168, z.data_ptr(), z.data_ptr(), z.data_ptr(), z.data_ptr(),
+            C.c_float(1e-6), c8.data_ptr(), c8.data_ptr(), None, None, z.data_ptr(), 1, 40, 8,
+            128, 16, 16, 16, 1, None]
+    assert R.lib().r4q_flash_decode_qkv(*args) == R.R4Q_EINVAL  # pos == max_seq
+    args[-3] = 15  # pos inside the cache ...
+    args[-4] = 8   # ... but past the RoPE table
+    assert R.lib().r4q_flash_decode_qkv(*args) == R.R4Q_EINVAL

@@ -8,8 +8,8 @@ import torch
 import int4_hip
 import r4q_synth as S
 from conftest import rel_l2
-from decode_util import (bench_args, build, check_forced_kv, gpu_kv_at, layer_args, oracle_step,
-                         step_logits)
+from decode_util import (bench_args, build, check_forced_kv, gpu_kv_at, layer_args,
+                         oracle_batch_forced, oracle_step, plan, step_logits)
 
 pytestmark = pytest.mark.gpu
 TOL = 5e-3
@@ -56,6 +56,93 @@ def test_qwen3_width_two_layers_vs_oracle(dev):
     logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(-1)
     assert np.all(np.isfinite(logits))
     assert rel_l2(logits, _oracle_forced(m, h, pos)) <= TOL
+
+
+def test_qwen3_width_batch8_step_vs_oracle(dev):
+    """Batch 8 at full Qwen3-14B width: skinny MFMA GEMMs with the step's own
+    split-K workspace, the gate/up split reduce applying SiLU + FWHT-32 (both
+    layers, INT4 and INT8), batched row norms; every row against the oracle
+    under KV teacher forcing."""
+    bits = {(0, "gu"): 8, (1, "down"): 8, (1, "qkv"): 8}
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=4096, max_seq=96, seed=13, bits=bits,
+              batch=8, fill=60, kv_scale=True)
+    nsplit, fused = plan(m, 8)
+    assert fused == 2, "batched gate/up did not take the fused SiLU reduce"
+    h = _hidden(m, 12, rows=8)
+    pos = 60
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(8, -1)
+    assert np.all(np.isfinite(logits))
+    _, want, n, total = oracle_batch_forced(m, h.numpy().reshape(8, -1), pos)
+    assert n <= 0.05 * total, f"{n} of {total} KV codes differ"
+    for b in range(8):
+        assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
+
+
+def test_qwen3_width_ctx2048_step_vs_oracle(dev):
+    """Batch 1 at ctx 2048 (position 2048, cache capacity 2088): the 17-split
+    attention with the head norm + RoPE + FP8 KV prologue in its owner
+    workgroup, against the oracle under KV teacher forcing."""
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=2048, max_seq=2088, seed=17,
+              bits={(1, "o"): 8}, fill=2048, kv_scale=True)
+    nsplit, fused = plan(m, 1)
+    assert nsplit == 17 and fused == 2, (nsplit, fused)
+    h = _hidden(m, 14)
+    pos = 2048
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(-1)
+    assert np.all(np.isfinite(logits))
+    assert rel_l2(logits, _oracle_forced(m, h, pos)) <= TOL
+
+
+@pytest.mark.parametrize("D,I,H,Hk,B", [(256, 512, 4, 2, 3), (5120, 17408, 40, 8, 1)])
+def test_graph_step_equals_eager_step(dev, D, I, H, Hk, B):
+    """decode_step_logits replays a captured step (the position set on the
+    device) by default: logits and KV bytes bit-identical to the eager
+    launches, at several positions through one cached graph."""
+    m = build(dev, D=D, I=I, H=H, Hk=Hk, L=2, vocab=1024, max_seq=80, seed=23, batch=B, fill=30,
+              bits={(0, "down"): 8})
+    h = _hidden(m, 9, rows=B).to(dev)
+    had = torch.zeros(32, 32, dtype=torch.float16, device=dev)
+    res = {}
+    for use_graph in (False, True):
+        m.reset_caches()
+        outs = []
+        for pos in (30, 31, 45):
+            lg = int4_hip.decode_step_logits(h, *layer_args(m, pos), m.k_caches, m.v_caches,
+                                             m.final_norm_d, m.lm_w_d, m.lm_s_d, m.vocab, m.D,
+                                             had, use_graph=use_graph)
+            hid = int4_hip.decode_step(h, *layer_args(m, pos + 1), m.k_caches, m.v_caches, had,
+                                       use_graph=use_graph)
+            outs.append((lg.cpu(), hid.cpu()))
+        res[use_graph] = (outs, [t.cpu() for t in m.k_caches + m.v_caches])
+    for (a, b), (c, d) in zip(res[False][0], res[True][0]):
+        assert torch.equal(a, c) and torch.equal(b, d)
+    for a, b in zip(res[False][1], res[True][1]):
+        assert torch.equal(a, b)
+
+
+def test_graph_loop_recaptures_after_sampling_workspace_moves(dev):
+    """A captured sampling loop bakes in the sampling workspace; a larger
+    r4q_sample call on the same context reallocates that workspace, so the
+    next replay must capture again rather than use the freed buffer.  The
+    tokens then equal the eager loop's."""
+    m = build(dev, D=256, I=512, H=4, Hk=2, L=2, vocab=700, max_seq=64, seed=29, fill=12)
+    h = _hidden(m, 10).to(dev)
+    had = torch.zeros(32, 32, dtype=torch.float16, device=dev)
+    kw = dict(temperature=0.8, top_p=0.9, seed=5)
+
+    def run(use_graph):
+        m.reset_caches()
+        return int4_hip.decode_loop(m.embed_d, m.final_norm_d, m.lm_w_d, m.lm_s_d, m.vocab, m.D,
+                                    h, 6, *layer_args(m, 12), m.k_caches, m.v_caches, had,
+                                    use_graph=use_graph, **kw)
+
+    first = run(True)
+    big = torch.randn(300, m.vocab, generator=S.gen(3)).half().to(dev)
+    int4_hip.sample(big, temperature=1.0, top_p=0.95, seed=1)  # grows the workspace
+    torch.cuda.synchronize()
+    again = run(True)
+    eager = run(False)
+    assert torch.equal(first, eager) and torch.equal(again, eager)
 
 
 def test_decode_step_hidden_matches_oracle(dev):
