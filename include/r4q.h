@@ -248,6 +248,23 @@ R4Q_API int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,
                      int64_t B, int64_t H, int64_t Hk, int64_t D,
                      int64_t max_seq, int64_t seq_len, int fwht, void* stream);
 
+/* r4q_flash_decode without a context and without any device allocation.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under hipGraph capture, serving loops and harnesses that forbid
+ * hipMalloc).  The split partials live in a fixed 4 MiB device array per GPU
+ * (held until the process ends), shared by every call on that GPU: calls
+ * that overlap on one GPU race and must be serialised by the caller.  A
+ * launch whose partials (B * H * splits * 528 bytes) exceed 4 MiB is
+ * rejected with R4Q_EINVAL; the default split counts stay below it for any
+ * GQA ratio up to 8.  The first call on each device looks up the array's
+ * device address (hipGetSymbolAddress), no allocation.  Same results as
+ * r4q_flash_decode, bit for bit. */
+R4Q_API int r4q_flash_decode_noalloc(const void* q, int64_t q_stride, const void* k_cache,
+                                     const void* v_cache, const float* k_scale,
+                                     const float* v_scale, void* out, int64_t B, int64_t H,
+                                     int64_t Hk, int64_t D, int64_t max_seq, int64_t seq_len,
+                                     int fwht, void* stream);
+
 /* The decode step's attention with its fused prologue, for one new position
  * `pos` of B sequences: qkv row b (at qkv + b*qkv_stride) holds the raw QKV
  * projection (q [H,D] | k [Hk,D] | v [Hk,D]); the kernel applies the

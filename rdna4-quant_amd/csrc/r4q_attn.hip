@@ -18,6 +18,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "r4q_ctx.hpp"
 #include "r4q_device.hpp"
@@ -651,4 +652,69 @@ extern "C" int r4q_flash_decode_qkv(r4q_ctx* ctx, const void* qkv, int64_t qkv_s
   return r4q::launch_flash_decode(qkv, qkv_stride, k_cache, v_cache, k_scale, v_scale, out, H * D,
                                   B, H, Hk, max_seq, pos + 1, nullptr, nsplit, fwht,
                                   static_cast<float*>(ctx->attn.ptr), r4q::as_stream(stream), &qk);
+}
+
+// ------------------------------------------------ allocation-free variant
+namespace r4q {
+namespace {
+// Split partials of r4q_flash_decode_noalloc: one array per GPU, alive until
+// the process ends, shared by every call on that GPU (calls that overlap on
+// one GPU race on it).  Every launch writes all the partials it reads, so
+// nothing has to start zeroed.
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (the host-side name is
+// only a stand-in): looked up once per device with hipGetSymbolAddress.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  R4Q_HIP_TRY(hipGetDevice(&dev));
+  R4Q_REQUIRE(dev >= 0 && dev < kMaxDevices, "flash_decode_noalloc: device %d out of range", dev);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      R4Q_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+      R4Q_REQUIRE(p, "flash_decode_noalloc: null scratch address");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return R4Q_OK;
+}
+}  // namespace
+}  // namespace r4q
+
+extern "C" int r4q_flash_decode_noalloc(const void* q, int64_t q_stride, const void* k_cache,
+                                        const void* v_cache, const float* k_scale,
+                                        const float* v_scale, void* out, int64_t B, int64_t H,
+                                        int64_t Hk, int64_t D, int64_t max_seq, int64_t seq_len,
+                                        int fwht, void* stream) {
+  R4Q_REQUIRE(q && k_cache && v_cache && out, "flash_decode_noalloc: null pointer");
+  R4Q_REQUIRE(D == 128, "flash_decode_noalloc: head_dim must be 128");
+  R4Q_REQUIRE(B >= 1 && H >= 1 && Hk >= 1 && H % Hk == 0, "flash_decode_noalloc: bad head counts");
+  R4Q_REQUIRE(seq_len >= 1 && seq_len <= max_seq,
+              "flash_decode_noalloc: seq_len %lld outside [1, %lld]", (long long)seq_len,
+              (long long)max_seq);
+  R4Q_REQUIRE(q_stride >= H * D && (q_stride % 8) == 0 &&
+                  (reinterpret_cast<uintptr_t>(q) & 15) == 0,
+              "flash_decode_noalloc: q rows must be 16-byte aligned with stride >= H*D");
+  R4Q_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15) == 0,
+              "flash_decode_noalloc: out must be 16-byte aligned");
+  const int nsplit = r4q::attn_num_splits(seq_len, B, Hk);
+  const size_t need = r4q::attn_ws_bytes(B, H, nsplit);
+  R4Q_REQUIRE(need <= r4q::kNoAllocScratchBytes,
+              "flash_decode_noalloc: %d splits x %lld heads x %lld sequences need %zu bytes of "
+              "partials, above the %zu-byte scratch",
+              nsplit, (long long)H, (long long)B, need, r4q::kNoAllocScratchBytes);
+  void* ws = nullptr;
+  R4Q_TRY(r4q::scratch_on_current_device(&ws));
+  return r4q::launch_flash_decode(q, q_stride, k_cache, v_cache, k_scale, v_scale, out, H * D, B,
+                                  H, Hk, max_seq, seq_len, nullptr, nsplit, fwht,
+                                  static_cast<float*>(ws), r4q::as_stream(stream));
 }

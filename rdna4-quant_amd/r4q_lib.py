@@ -92,6 +92,8 @@ SIGNATURES = {
     "r4q_ctx_destroy": [_p],
     "r4q_flash_decode": [_p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                          _i64, C.c_int, _p],
+    "r4q_flash_decode_noalloc": [_p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64,
+                                 _i64, C.c_int, _p],
     "r4q_flash_decode_qkv": [_p, _p, _i64, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p, _i64,
                              _i64, _i64, _i64, _i64, _i64, _i64, C.c_int, _p],
     "r4q_decode_step": [_p, C.POINTER(R4QModel), _p, _i64, _i64, _p, _p, _p],
