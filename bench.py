@@ -12,9 +12,11 @@ Also measured in the same run:
     events on the stream the library launches on, cycling 8 weight copies so
     the 256 MB last-level cache cannot hold them; algorithmic bytes per
     launch = packed weights + 3 B per 32-element block + x in + y out;
-  * cpu_baseline: the numpy oracle (the reference's dequant + matmul +
-    attention path restated) on the host cores, on one full-width layer at
-    ctx=2048 plus the LM head, extrapolated to 40 layers.
+  * cpu_baseline: the reference's torch path (per-matrix dequant, x @ w.T,
+    SDPA over the decoded FP8 KV; oracle/r4q_torch_ref.py) on the host
+    cores, median of 5 runs per piece, summed to a 40-layer token;
+  * engine_ms_per_token: the engine's own per-token loop (embedding,
+    decode_step_logits, argmax, .item()).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 2048]
        [--batch 1] [--no-cpu-baseline]
@@ -207,7 +209,8 @@ def prefill_gemm_leg(dev, iters=20):
 
 
 def flash_decode_leg(dev, ctx, iters=100):
-    """Config 2: r4q_flash_decode at batch 1, 40 query / 8 KV heads, cold KV.
+    """Config 2: r4q_flash_decode at batch 1, 40 query / 8 KV heads, FP8 KV
+    with per-head fp32 scales, cold KV.
 
     A ring of KV cache pairs larger than 512 MB (more than the 256 MB
     last-level cache) is cycled by `iters` launches captured in one hipGraph
@@ -232,6 +235,9 @@ def flash_decode_leg(dev, ctx, iters=100):
         v = torch.randint(0, 0x40, (Hk, max_seq, D), dtype=torch.uint8, device=dev, generator=g)
         caches.append((k, v))
     q = torch.randn(H * D, device=dev, generator=g).half()
+    # per-head fp32 K / V scales (config 2)
+    ksc = (0.5 + torch.rand(Hk, device=dev, generator=g)).float()
+    vsc = (0.5 + torch.rand(Hk, device=dev, generator=g)).float()
     out = torch.empty(H * D, dtype=torch.float16, device=dev)
     ctx_h = C.c_void_p()
     R.call("r4q_ctx_create", C.byref(ctx_h))
@@ -239,8 +245,9 @@ def flash_decode_leg(dev, ctx, iters=100):
 
     def launch(i):
         k, v = caches[i % ncopy]
-        R.call("r4q_flash_decode", ctx_h, q.data_ptr(), H * D, k.data_ptr(), v.data_ptr(), None,
-               None, out.data_ptr(), 1, H, Hk, D, max_seq, ctx, 1, st.cuda_stream)
+        R.call("r4q_flash_decode", ctx_h, q.data_ptr(), H * D, k.data_ptr(), v.data_ptr(),
+               ksc.data_ptr(), vsc.data_ptr(), out.data_ptr(), 1, H, Hk, D, max_seq, ctx, 1,
+               st.cuda_stream)
 
     launch(0)
     torch.cuda.synchronize()
@@ -277,47 +284,167 @@ def copy_calibration(dev, mib=256, iters=20):
     return mib * (1 << 20)
 
 
-def cpu_baseline(m, ctx):
-    """Oracle (numpy) time per token on the host, from one full-width layer at
-    `ctx` plus the LM head, extrapolated to all layers."""
+def _cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on,
+    capped at OMP_NUM_THREADS when that is set (the box's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return (min(n, int(cap)) if cap.isdigit() and int(cap) > 0 else n), n
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(m, ctx, reps=5):
+    """The reference's torch path on the host cores (r4q_torch_ref: the
+    engine's own torch operations restated), median of `reps` runs after one
+    warm-up each:
+      * config 4 (value): a batch-1 token with every projection dequantised
+        on the fly before its `x @ w.T` (fast_prefill's per-matrix dequant,
+        int4_engine_v5.py:214-266): each (projection, precision) timed once
+        as dequant + matvec, attention (SDPA over the decoded FP8 KV at
+        `ctx`) + norms + RoPE timed on one layer, summed over the 40 layers
+        of the seeded INT4/INT8 mask, plus the FP16 LM head;
+      * the same token with pre-dequantised FP16 weights (one layer's
+        matrices dequantised once and timed, x 40; the whole 28 GB model is
+        not materialised);
+      * configs 0-3 as single calls."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
+    import statistics
+
     import torch
 
-    import r4q_oracle as O
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    except Exception:
-        threads = 1
-    a = m["args"]
-    li = 0
-    ly = O.Layer(**{n + k: (a[n + k][li].cpu().numpy() if a[n + k][li] is not None else None)
-                    for n in ("qkv", "o", "gu", "down") for k in ("_w", "_s")},
-                 **{n + "_bits": m["mask"][(li, n)] for n in ("qkv", "o", "gu", "down")},
-                 in_norm=a["in_norm"][li].cpu().numpy(), post_norm=a["post_norm"][li].cpu().numpy(),
-                 q_norm=a["q_norm"][li].cpu().numpy(), k_norm=a["k_norm"][li].cpu().numpy())
-    for n in ("qkv", "o", "gu", "down"):
-        s = getattr(ly, n + "_s")
-        if s is not None:
-            setattr(ly, n + "_s", s.reshape(s.shape[0], -1, 2))
-    kc = [m["kc"][li][0].cpu().numpy()]
-    vc = [m["vc"][li][0].cpu().numpy()]
-    h = (torch.randn(m["D"], generator=torch.Generator().manual_seed(1)) * 0.5).half().numpy()
-    cos, sin = m["cos"].cpu().numpy(), m["sin"].cpu().numpy()
-    t0 = time.perf_counter()
-    O.decode_step([ly], h, ctx - 1, kc, vc, H=m["H"], Hk=m["Hk"], D=m["hd"], hidden=m["D"],
-                  inter=m["I"], eps=m["eps"], rope_cos=cos, rope_sin=sin)
-    t_layer = time.perf_counter() - t0
-    lm = m["lm_w"].cpu().numpy()
-    t0 = time.perf_counter()
-    O.gemv(O.rmsnorm_fwht(h, m["final_norm"].cpu().numpy(), m["eps"]), lm, None, 16)
-    t_lm = time.perf_counter() - t0
-    t_tok = m["L"] * t_layer + t_lm
+    import r4q_synth as S
+    import r4q_torch_ref as TR
+    threads, affinity = _cpu_threads()
+    torch.set_num_threads(threads)
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    D, I, H, Hk = m["D"], m["I"], m["H"], m["Hk"]
+    g = S.gen(7)
+    shapes = {"qkv": ((H + 2 * Hk) * 128, D), "o": (D, H * 128), "gu": (2 * I, D), "down": (D, I)}
+    x = {n: S.rotated_activation(K, g)[:1] for n, (_, K) in shapes.items()}
+    t_fly, t_mm, mats = {}, {}, {}
+    with torch.inference_mode():
+        for n, (N, K) in shapes.items():
+            for bits in (4, 8):
+                w, sz = S.weight(N, K, bits, g)
+                t_fly[(n, bits)] = med(lambda: TR.mm_ref(x[n], TR.dequant(w, sz, bits)))
+                if bits == 4:
+                    mats[n] = (w, sz)
+                    w16 = TR.dequant(w, sz, 4)
+                    t_mm[n] = med(lambda: TR.mm_ref(x[n], w16))
+                del w, sz
+        # one INT4 layer with pre-dequantised weights: attention at ctx + norms
+        ly = type("L", (), {})()
+        for n in shapes:
+            setattr(ly, n + "_w", mats[n][0])
+            setattr(ly, n + "_s", mats[n][1])
+            setattr(ly, n + "_bits", 4)
+        for n in ("in_norm", "post_norm"):
+            setattr(ly, n, S.norm_weight(D, g))
+        ly.q_norm, ly.k_norm = S.norm_weight(128, g), S.norm_weight(128, g)
+        wts = {n: TR.dequant(*mats[n], 4) for n in shapes}
+        cap = ctx + 8
+        kc = torch.randint(0, 0x40, (Hk, cap, 128), dtype=torch.uint8, generator=g)
+        vc = torch.randint(0, 0x40, (Hk, cap, 128), dtype=torch.uint8, generator=g)
+        cos, sin = S.rope_tables(128, cap)
+        lut, had = TR.fp8_table(), TR.hadamard_fp16()
+        h = (torch.randn(1, D, generator=g) * 0.5).half()
+        kw = dict(eps=m["eps"], H=H, Hk=Hk, I=I, lut=lut, had=had)
+        t_layer_pre = med(lambda: TR.decode_layer(h, ly, ctx - 1, kc, vc, cos, sin, wts=wts, **kw))
+        t_rest = max(0.0, t_layer_pre - sum(t_mm.values()))
+        del wts
+        lm = m["lm_w"].cpu()
+        xl = S.rotated_activation(D, g)[:1]
+        t_lm = med(lambda: TR.mm_ref(xl, lm))
+        del lm
+        L = m["L"]
+        t_tok = L * t_rest + t_lm + sum(t_fly[(n, m["mask"][(li, n)])]
+                                        for li in range(L) for n in shapes)
+        t_tok_pre = L * t_layer_pre + t_lm
+
+        # configs 0-3, one call each
+        w0, sz0 = S.int4_weight(17408, 5120, S.gen(0))
+        x0 = S.rotated_activation(5120, S.gen(0))[:1]
+        t0c = med(lambda: TR.mm_ref(x0, TR.dequant(w0, sz0, 4)))
+        del w0, sz0
+        c1 = t_rest + t_fly[("qkv", 4)] + t_fly[("o", 4)] + t_fly[("gu", 4)] + t_fly[("down", 8)]
+        attn = {}
+        for c in (2048, 32768):
+            kq = torch.randint(0, 0x40, (1, Hk, c, 128), dtype=torch.uint8, generator=g)
+            vq = torch.randint(0, 0x40, (1, Hk, c, 128), dtype=torch.uint8, generator=g)
+            q = torch.randn(1, H, 1, 128, generator=g).half()
+            ta = med(lambda: torch.nn.functional.scaled_dot_product_attention(
+                q.float(), lut[kq.long()], lut[vq.long()], enable_gqa=True).half())
+            kvb = 2 * Hk * 128 * c
+            attn[str(c)] = {"ms": round(ta * 1e3, 3), "gbps": round(kvb / ta / 1e9, 2)}
+            del kq, vq
+        gemm = {}
+        for K, N in ((5120, 17408), (17408, 5120)):
+            w3, sz3 = S.int4_weight(N, K, S.gen(3))
+            X = torch.randn(512, K, generator=S.gen(3)).half()
+            t3 = med(lambda: TR.mm_ref(X, TR.dequant(w3, sz3, 4)))
+            gemm[f"{K}x{N}"] = {"ms": round(t3 * 1e3, 2),
+                                "tflops": round(2 * 512 * N * K / t3 / 1e12, 3)}
+            del w3, sz3
     return {"value": round(1.0 / t_tok, 5), "unit": "tok/s", "cores": int(threads),
             "kind": "port",
-            "sample": (f"numpy oracle: 1 full-width layer at ctx={ctx} ({t_layer:.2f} s) x "
-                       f"{m['L']} + FP16 LM head ({t_lm:.2f} s), batch 1")}
+            "sample": (f"torch restatement of the engine's path (r4q_torch_ref), {threads} "
+                       f"threads, median of {reps}: per-matrix dequant + x @ w.T for each "
+                       f"projection shape in INT4 and INT8, attention over the decoded FP8 KV "
+                       f"at ctx={ctx} + norms on one layer, summed over {L} layers of the "
+                       f"seeded mask + FP16 LM head ({t_tok:.1f} s/token)"),
+            "cpu_model": _cpu_model(), "threads": int(threads), "affinity_cpus": int(affinity),
+            "median_of": reps,
+            "predequant_fp16_tok_s": round(1.0 / t_tok_pre, 4),
+            "predequant_note": "one layer's matrices dequantised once and timed, x 40 + LM head",
+            "config0_ms": round(t0c * 1e3, 2),
+            "config0_gbps": round(52965376 / t0c / 1e9, 3),
+            "config1_ms": round(c1 * 1e3, 2),
+            "config2": attn,
+            "config3": gemm}
+
+
+def engine_leg(m, ctx, tokens=32, warm=4):
+    """The engine's per-token loop (int4_engine_v5.py:343-355): embedding,
+    decode_step_logits, logits[0, 0].float().argmax(), .item(), position + 1.
+    Returns ms per token over `tokens` tokens after `warm` untimed ones."""
+    import torch
+    import torch.nn.functional as F
+
+    import int4_hip
+    args = list(bench_args(m, ctx))
+    embed = m["embed"]
+    nid = torch.ones(1, 1, dtype=torch.long, device=embed.device)
+    pos = ctx
+    t0 = None
+    for i in range(warm + tokens):
+        if i == warm:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+        hidden = F.embedding(nid.view(1), embed).view(1, 1, m["D"])
+        args[18] = pos
+        logits = int4_hip.decode_step_logits(hidden, *args)
+        nid = logits[0, 0, :].float().argmax(-1, keepdim=True).unsqueeze(0)
+        _ = nid.item()
+        pos += 1
+    return (time.perf_counter() - t0) * 1e3 / tokens
 
 
 def main():
@@ -331,6 +458,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the config-3 prefill GEMM leg (the program the MFMA "
                          "counter runs profile)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the config-4 decode leg (the program the decode kernel "
+                         "trace profiles)")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline GEMV loop and the copy calibration "
                          "(the program the counter runs profile)")
@@ -356,21 +486,23 @@ def main():
                           "read_floor_bytes": rf_bytes, "copy_bytes": nbytes}), flush=True)
         return
     # the config-0 GEMV first, on a GPU not yet holding the 11 GB model
-    us, alg = gemv_roofline(dev)
-    gbps = alg / us / 1e3
-    rf_us, rf_bytes = read_floor(dev)
-    log(f"INT4 GEMV 5120->17408: {us:.2f} us, {gbps:.0f} GB/s; plain read of its "
-        f"{rf_bytes} bytes: {rf_us:.2f} us")
+    us = alg = gbps = rf_us = None
+    if not args.decode_only:
+        us, alg = gemv_roofline(dev)
+        gbps = alg / us / 1e3
+        rf_us, rf_bytes = read_floor(dev)
+        log(f"INT4 GEMV 5120->17408: {us:.2f} us, {gbps:.0f} GB/s; plain read of its "
+            f"{rf_bytes} bytes: {rf_us:.2f} us")
 
     attn = {}
-    for c in (128, 2048, 8192, 32768):
+    for c in (() if args.decode_only else (128, 2048, 8192, 32768)):
         a_us, a_bytes = flash_decode_leg(dev, c)
         attn[str(c)] = {"us": round(a_us, 3), "kv_bytes": a_bytes,
                         "gbps": round(a_bytes / a_us / 1e3, 1),
                         "frac": round(a_bytes / a_us / 1e3 / HBM_PEAK_GBPS, 4)}
         log(f"flash-decode ctx={c}: {a_us:.2f} us, {a_bytes / a_us / 1e3:.0f} GB/s (cold KV)")
     torch.cuda.empty_cache()
-    pgemm = prefill_gemm_leg(dev)
+    pgemm = {} if args.decode_only else prefill_gemm_leg(dev)
     for k, v in pgemm.items():
         log(f"prefill GEMM 512x{k.replace('x', ' -> ')} INT4: {v['us']:.1f} us, "
             f"{v['tflops']:.0f} TFLOP/s ({v['frac'] * 100:.1f}% of fp16 MFMA peak)")
@@ -402,6 +534,16 @@ def main():
     ms = dt * 1000.0 / args.steps
     tok_s = args.batch * args.steps / dt
     log(f"decode: {ms:.3f} ms/step, {tok_s:.1f} tok/s")
+    eng_ms = None
+    if args.batch == 1:
+        gc.disable()
+        eng_ms = engine_leg(m, args.ctx)
+        gc.enable()
+        log(f"engine loop (decode_step_logits + argmax + .item()): {eng_ms:.3f} ms/token")
+    if args.decode_only:
+        print(json.dumps({"ms_per_step": round(ms, 4), "tok_s": round(tok_s, 3),
+                          "ctx": args.ctx, "batch": args.batch}), flush=True)
+        return
 
     # prompt pass: 512 tokens through all layers + LM head for every row
     # (config 3's GEMM shapes inside the full prefill)
@@ -427,7 +569,7 @@ def main():
     step_bytes = m["wbytes"] + m["lm_bytes"] + kv_bytes
     cpu = None
     if not args.no_cpu_baseline:
-        log("timing the CPU oracle (one layer + LM head)")
+        log("timing the reference's torch path on the host CPU")
         cpu = cpu_baseline(m, args.ctx)
         log(f"cpu baseline: {cpu['value']} tok/s")
 
@@ -457,6 +599,10 @@ def main():
         "step_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "int4_gemv_gbps": round(gbps, 1),
         "prefill_512_tok_s": round(pre_m / pre_s, 1),
+        # the engine's own per-token path: eager decode_step_logits call (a
+        # replayed graph inside), argmax and .item() per token, at ctx
+        "engine_ms_per_token": None if eng_ms is None else round(eng_ms, 4),
+        "engine_tok_s": None if eng_ms is None else round(1e3 / eng_ms, 2),
         "roofline": {
             "kernel": f"INT4 GEMV K=5120 -> N=17408 ({ROOFLINE_KERNEL})",
             "bound": "hbm",

@@ -15,14 +15,12 @@ layer's or the wrong norm's gamma) moves results far beyond the tolerance.
 The two routes round in different places (the reference rounds the norm to
 fp16 before the Hadamard matmul, the kernels after), so they agree to
 rel-L2 <= 5e-3, not bit for bit."""
-import math
-
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 import r4q_oracle as O
+import r4q_torch_ref as TR
 from conftest import rel_l2
 
 TOL = 5e-3
@@ -58,67 +56,8 @@ def _model(seed):
     return layers, embed, final, lm_w, lm_s, ids
 
 
-# ---------------------------------------------------------- torch restatement
-def _t_dequant(packed, sz):
-    """dequantize_int4_asym (int4_quant_v2.py:97-127): unpack lo/hi nibbles,
-    (q - zp) * scale in fp32, then fp16."""
-    p = torch.from_numpy(packed)
-    q = torch.stack([p & 0x0F, (p >> 4) & 0x0F], -1).reshape(p.shape[0], -1).float()
-    s = torch.from_numpy(sz[..., 0].astype(np.float32)).repeat_interleave(32, 1)
-    z = torch.from_numpy(sz[..., 1].astype(np.float32)).repeat_interleave(32, 1)
-    return ((q - z) * s).half()
-
-
-def _t_mm(x16, w16):
-    """x @ w.T as an fp16 GEMM with fp32 accumulation (rocBLAS / hipBLASLt)."""
-    return (x16.float() @ w16.float().T).half()
-
-
 def _t_prefill(layers, embed, final, lm_w, lm_s, ids, cos, sin):
-    had = torch.from_numpy(O.hadamard_matrix(32) / math.sqrt(32)).float().half()
-
-    def fast_hadamard(x):
-        return _t_mm(x.reshape(-1, 32), had.T).reshape(x.shape)
-
-    def fast_rmsnorm(x, w):
-        var = x.float().pow(2).mean(-1, keepdim=True)
-        return (x.float() * torch.rsqrt(var + EPS) * w.float()).half()
-
-    def head_rmsnorm(x, w):
-        var = x.float().pow(2).mean(-1, keepdim=True)
-        return (x.float() * torch.rsqrt(var + EPS) * w.float()).half()
-
-    def apply_rope(x, pos):  # x [1, nh, M, 128] fp16, half-split
-        c = cos[pos].unsqueeze(1)
-        s = sin[pos].unsqueeze(1)
-        x1, x2 = x[..., :64], x[..., 64:]
-        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], -1)
-
-    T = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
-    pos = torch.arange(M).unsqueeze(0)
-    x = T(embed)[torch.from_numpy(ids)]
-    trace = []
-    qd, kd = H * 128, Hk * 128
-    for ly in layers:
-        normed = fast_hadamard(fast_rmsnorm(x, T(ly.in_norm)))
-        qkv = _t_mm(normed, _t_dequant(ly.qkv_w, ly.qkv_s))
-        q = head_rmsnorm(qkv[:, :qd].view(M, H, 128), T(ly.q_norm))
-        k = head_rmsnorm(qkv[:, qd:qd + kd].view(M, Hk, 128), T(ly.k_norm))
-        v = qkv[:, qd + kd:].view(M, Hk, 128)
-        q = apply_rope(q.unsqueeze(0).transpose(1, 2), pos)
-        k = apply_rope(k.unsqueeze(0).transpose(1, 2), pos)
-        v = v.unsqueeze(0).transpose(1, 2)
-        att = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True,
-                                             enable_gqa=True).half()
-        att = att.squeeze(0).transpose(0, 1).reshape(M, qd)
-        x = x + _t_mm(fast_hadamard(att), _t_dequant(ly.o_w, ly.o_s))
-        normed = fast_hadamard(fast_rmsnorm(x, T(ly.post_norm)))
-        gu = _t_mm(normed, _t_dequant(ly.gu_w, ly.gu_s))
-        mlp = F.silu(gu[:, :I]) * gu[:, I:]
-        x = x + _t_mm(fast_hadamard(mlp), _t_dequant(ly.down_w, ly.down_s))
-        trace.append(x.numpy().copy())
-    normed = fast_hadamard(fast_rmsnorm(x, T(final)))
-    return trace, _t_mm(normed, _t_dequant(lm_w, lm_s)).numpy()
+    return TR.prefill(layers, embed, final, lm_w, lm_s, ids, cos, sin, eps=EPS, H=H, Hk=Hk, I=I)
 
 
 def _common(final, lm_w, lm_s, cos, sin):
