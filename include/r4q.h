@@ -368,8 +368,8 @@ R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hid
 /* Measurement aid with no counterpart in the reference: overrides one
  * launch-shape choice for the whole process (value 0 restores the built-in
  * choice).  Knobs: "gemv_lpr" (lanes per GEMV row: 16..256, power of two),
- * "gemv_wgs" (GEMV workgroup cap, 1..65536), "gemv_ub" (GEMV steps per batch,
- * 1..2), "attn_splits" (flash-decode splits, 1..128), "skinny_splits"
+ * "gemv_wgs" (GEMV workgroup cap, 1..65536), "gemv_ub" (GEMV steps in flight
+ * per lane, 1..2), "attn_splits" (flash-decode splits, 1..128), "skinny_splits"
  * (skinny GEMM K splits, 1..8), "gemm_splits" (ring GEMM K splits of every
  * tile, 1..16).  Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS,
  * R4Q_GEMV_UB, R4Q_ATTN_SPLITS, R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, read once.

@@ -29,6 +29,8 @@
 //    LDS once, at the end of the workgroup.
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "r4q_device.hpp"
 #include "r4q_gemv.hpp"
 #include "r4q_host.hpp"
@@ -210,11 +212,57 @@ __device__ __forceinline__ void lds_copy(const uint32_t* __restrict__ src, uint3
   }
 }
 
-// Shared prologue: arrange x into LDS (every thread of the workgroup).
-template <int WBITS>
-__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, uint32_t* xs, int cpr) {
-  for (int c = threadIdx.x; c < cpr; c += blockDim.x)
-    prep_chunk<WBITS>(x, c, xs + c * Fmt<WBITS>::kXDw);
+// Plain staging: x as fp16.  Thread t arranges chunks t, t + 256, ... (at
+// most NPC); their loads are requested before the first weight steps (see
+// NormIn), at clamped addresses so that they are straight-line code.
+template <int WBITS, int LPR, int CPL>
+struct PlainIn {
+  static constexpr int XD = Fmt<WBITS>::kXDw;
+  static constexpr int kRow = (LPR * CPL + 255) / 256;      // chunks a row of this shape has
+  static constexpr int kLds = (65536 / (XD * 4) + 255) / 256;  // chunks the LDS stage holds
+  static constexpr int NPC = kRow < kLds ? kRow : kLds;
+  static constexpr int W = Fmt<WBITS>::kElems / 2;  // dwords per chunk
+  uint32_t raw[NPC][W];
+};
+
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void plain_issue(const uint16_t* __restrict__ x,
+                                            PlainIn<WBITS, LPR, CPL>& in, int cpr) {
+  using P = PlainIn<WBITS, LPR, CPL>;
+#pragma unroll
+  for (int i = 0; i < P::NPC; ++i) {
+    const int c = min((int)threadIdx.x + 256 * i, cpr - 1);
+    const u4_t* src = reinterpret_cast<const u4_t*>(x + (int64_t)c * Fmt<WBITS>::kElems);
+#pragma unroll
+    for (int q = 0; q < P::W / 4; ++q) {
+      const u4_t v = src[q];
+      in.raw[i][4 * q] = v[0];
+      in.raw[i][4 * q + 1] = v[1];
+      in.raw[i][4 * q + 2] = v[2];
+      in.raw[i][4 * q + 3] = v[3];
+    }
+  }
+}
+
+// The plain staging's counterpart of norm_pin.
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void plain_pin(PlainIn<WBITS, LPR, CPL>& in) {
+  using P = PlainIn<WBITS, LPR, CPL>;
+#pragma unroll
+  for (int i = 0; i < P::NPC; ++i)
+#pragma unroll
+    for (int k = 0; k < P::W; ++k) asm volatile("" : "+v"(in.raw[i][k])::"memory");
+}
+
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void stage_x(const PlainIn<WBITS, LPR, CPL>& in, uint32_t* xs,
+                                        int cpr) {
+  using P = PlainIn<WBITS, LPR, CPL>;
+#pragma unroll
+  for (int i = 0; i < P::NPC; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c < cpr) prep_raw<WBITS>(in.raw[i], xs + c * P::XD);
+  }
   __syncthreads();
 }
 
@@ -235,33 +283,66 @@ struct GemvNorm {
   int split;
 };
 
+// Inputs of the fused-norm staging, requested before the first weight steps:
+// loads retire in issue order, so activation loads issued after the weights
+// would hold the staging arithmetic until every prefetched weight step had
+// landed.  Every thread loads (its chunk clamped to the last one, and x in
+// place of a missing residual), so the loads are straight-line code.
+struct NormIn {
+  uint32_t g[16], a[16], b[16];
+};
+
+__device__ __forceinline__ void norm_issue(const uint16_t* __restrict__ x, const GemvNorm& nm,
+                                           NormIn& in, int K) {
+  const int c = min((int)threadIdx.x, K / 32 - 1);
+  load16w(nm.gamma + c * 32, in.g);
+  load16w(x + c * 32, in.a);
+  load16w((nm.b ? nm.b : x) + c * 32, in.b);
+}
+
+// Marks the fused-norm inputs as consumed here: the empty asm statements
+// (memory clobber) keep the weight loads issued above them and the norm
+// arithmetic below, so the wait they imply covers only the earlier
+// activation loads.
+__device__ __forceinline__ void norm_pin(NormIn& in) {
+  asm volatile("" : "+v"(in.g[0]), "+v"(in.g[1]), "+v"(in.g[2]), "+v"(in.g[3]), "+v"(in.g[4]),
+               "+v"(in.g[5]), "+v"(in.g[6]), "+v"(in.g[7]), "+v"(in.g[8]), "+v"(in.g[9]),
+               "+v"(in.g[10]), "+v"(in.g[11]), "+v"(in.g[12]), "+v"(in.g[13]), "+v"(in.g[14]),
+               "+v"(in.g[15])::"memory");
+  asm volatile("" : "+v"(in.a[0]), "+v"(in.a[1]), "+v"(in.a[2]), "+v"(in.a[3]), "+v"(in.a[4]),
+               "+v"(in.a[5]), "+v"(in.a[6]), "+v"(in.a[7]), "+v"(in.a[8]), "+v"(in.a[9]),
+               "+v"(in.a[10]), "+v"(in.a[11]), "+v"(in.a[12]), "+v"(in.a[13]), "+v"(in.a[14]),
+               "+v"(in.a[15])::"memory");
+  asm volatile("" : "+v"(in.b[0]), "+v"(in.b[1]), "+v"(in.b[2]), "+v"(in.b[3]), "+v"(in.b[4]),
+               "+v"(in.b[5]), "+v"(in.b[6]), "+v"(in.b[7]), "+v"(in.b[8]), "+v"(in.b[9]),
+               "+v"(in.b[10]), "+v"(in.b[11]), "+v"(in.b[12]), "+v"(in.b[13]), "+v"(in.b[14]),
+               "+v"(in.b[15])::"memory");
+}
+
 template <int WBITS>
-__device__ __forceinline__ void stage_x_norm(const uint16_t* __restrict__ x, const GemvNorm& nm,
-                                             uint32_t* xs, float* red, int K) {
+__device__ __forceinline__ void stage_x_norm(const NormIn& in, const GemvNorm& nm, uint32_t* xs,
+                                             float* red, int K) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
   const int c = threadIdx.x;
   const bool act = c < K / 32;
-  uint32_t g[16], r[16];
-  float ss = 0.f;
-  if (act) {
-    uint32_t av[16], bv[16];
-    load16w(nm.gamma + c * 32, g);  // requested with the activation
-    load16w(x + c * 32, av);
-    if (nm.b) {
-      load16w(nm.b + c * 32, bv);
-      ss = norm_chunk_sumsq<true>(av, bv, r, ss);
-    } else {
-      ss = norm_chunk_sumsq<false>(av, bv, r, ss);
-    }
-  }
+  // Without a residual, b is -0: fp16 a + (-0) == a and fp32(a) + (-0) ==
+  // fp32(a) exactly, so one code path serves both.  Every thread computes
+  // (idle ones on a clamped chunk, masked below): the loads are used
+  // unconditionally and cannot sink behind the weight loads.
+  uint32_t b[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) b[k] = nm.b ? in.b[k] : 0x80008000u;
+  uint32_t r[16];
+  float ss = norm_chunk_sumsq<true>(in.a, b, r, 0.f);
+  ss = act ? ss : 0.f;
   const float tot = block_sum(ss, red);
   const float rrms = 1.0f / __builtin_sqrtf(tot / (float)K + nm.eps);
   if (act) {
     // the residual is rounded to fp16 before normalisation
     if (nm.b && blockIdx.x == 0) store16w(nm.res_out + c * 32, r);
     uint32_t raw[16];
-    norm_chunk_scale<true>(r, g, rrms, raw);
+    norm_chunk_scale<true>(r, in.g, rrms, raw);
 #pragma unroll
     for (int sub = 0; sub < 32 / E; ++sub)
       prep_raw<WBITS>(raw + sub * (E / 2), xs + (c * (32 / E) + sub) * XD);
@@ -328,9 +409,9 @@ __device__ __forceinline__ uint32_t load_sz(const uint32_t* __restrict__ srow, i
 // lanes share a row (LPR <= 64: inside one wave; 128/256: 2/4 waves) and
 // lane `cl` of a row owns chunk columns cl + LPR*i, i < CPL (columns past the
 // row end are masked).  A RowMap gives the first row of the workgroup's k-th
-// step; UB consecutive steps form a batch.  The first batch is requested
-// before the activation is staged, so that staging hides behind the weight
-// stream.
+// step.  The tile is a ring of UB register slots, one step each; the first
+// UB steps are requested before the activation is staged, so that staging
+// hides behind the weight stream.
 template <int WBITS, int LPR, int CPL, int UB>
 struct GemvTile {
   static constexpr int RPS = 256 / LPR;
@@ -384,7 +465,7 @@ __device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
                                           int nloc, int rs, int cl) {
 #pragma unroll
   for (int j = 0; j < UB; ++j) {
-    const int k = min(k0 + j, nloc - 1);  // clamped: in bounds
+    const int k = max(0, min(k0 + j, nloc - 1));  // clamped: in bounds
     const int rowc = min(map.row0(k) + rs, N - 1);
     const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes);
     const uint32_t* srow = sz + (int64_t)rowc * nb;
@@ -466,46 +547,24 @@ __device__ __forceinline__ void gemv_finish(float acc, uint16_t* __restrict__ y,
   }
 }
 
-// Computes the UB steps of a batch.
-template <int WBITS, int LPR, int CPL, int UB, class Map, int EPI>
-__device__ __forceinline__ void gemv_compute(const GemvTile<WBITS, LPR, CPL, UB>& t,
-                                             const uint32_t* __restrict__ xr,
-                                             uint16_t* __restrict__ y, float* red, float* ut,
-                                             int cpr, int N, const Map& map, int k0, int nloc,
-                                             int rs, int cl) {
-  constexpr int XD = Fmt<WBITS>::kXDw;
-#pragma unroll
-  for (int j = 0; j < UB; ++j) {
-    const int k = k0 + j;
-    if (k >= nloc) break;  // workgroup-uniform
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      if (LPR * CPL <= cpr || cl + LPR * i < cpr)
-        acc = chunk_dot<WBITS>(t.wq[j][i], t.s2[j][i], xr + i * XD, acc);
-    }
-    gemv_finish<LPR, Map, EPI>(acc, y, red, ut, N, map, k, rs, cl);
-  }
-}
-
-// One step with a rolling prefetch: as soon as chunk i of step k has been
-// consumed, its register is refilled with chunk i of step k + 1, so the next
-// step's loads overlap this step's arithmetic while no lane holds more than
-// one step's chunks in flight.
+// One step from a slot of the register ring (wq / s2: CPL chunks and their
+// (scale, zero) words) with a rolling refill: as soon as chunk i of step k
+// has been consumed, its register receives chunk i of step kn, so the loads
+// of the steps ahead overlap this step's arithmetic.
 template <int WBITS, int LPR, int CPL, class Map, int EPI, bool NEXT>
-__device__ __forceinline__ void gemv_step_roll(GemvTile<WBITS, LPR, CPL, 1>& t,
+__device__ __forceinline__ void gemv_step_roll(u4_t (&wq)[CPL], uint32_t (&s2)[CPL],
                                                const uint32_t* __restrict__ xr,
                                                const uint8_t* __restrict__ w,
                                                const uint32_t* __restrict__ sz,
                                                int64_t row_bytes, int nb,
                                                uint16_t* __restrict__ y, float* red, float* ut,
-                                               int cpr, int N, const Map& map, int k, int rs,
-                                               int cl) {
+                                               int cpr, int N, const Map& map, int k, int kn,
+                                               int rs, int cl) {
   constexpr int XD = Fmt<WBITS>::kXDw;
   const u4_t* wrow = nullptr;
   const uint32_t* srow = nullptr;
   if constexpr (NEXT) {
-    const int rown = min(map.row0(k + 1) + rs, N - 1);
+    const int rown = min(map.row0(kn) + rs, N - 1);
     wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rown * row_bytes);
     srow = sz + (int64_t)rown * nb;
   }
@@ -513,19 +572,15 @@ __device__ __forceinline__ void gemv_step_roll(GemvTile<WBITS, LPR, CPL, 1>& t,
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     if (LPR * CPL <= cpr || cl + LPR * i < cpr)
-      acc = chunk_dot<WBITS>(t.wq[0][i], t.s2[0][i], xr + i * XD, acc);
+      acc = chunk_dot<WBITS>(wq[i], s2[i], xr + i * XD, acc);
     if constexpr (NEXT) {
       const int c = min(cl + LPR * i, cpr - 1);
-      t.wq[0][i] = load_nt(wrow + c);
-      t.s2[0][i] = load_sz<WBITS>(srow, c);
+      wq[i] = load_nt(wrow + c);
+      s2[i] = load_sz<WBITS>(srow, c);
     }
   }
   gemv_finish<LPR, Map, EPI>(acc, y, red, ut, N, map, k, rs, cl);
 }
-
-// Main-loop schedule: rolling prefetch (one step per iteration) when true,
-// else load-then-compute batches of UB steps.
-constexpr bool kRollingPrefetch = true;
 
 template <int WBITS, int LPR, int CPL, int UB, int XM, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ x,
@@ -553,16 +608,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   map.h = nm.h;
   const int nloc = map.nlocal();
 
+  NormIn nin;
+  PlainIn<WBITS, LPR, CPL> pin;
+  if constexpr (XM == kXNorm) norm_issue(x, nm, nin, K);
+  else if constexpr (XM == kXPlain) plain_issue(x, pin, cpr);
+  // the first UB steps (unconditional and clamped, so that the compiler's
+  // wait counts stay exact: a workgroup without steps re-reads a valid row)
   GemvTile<WBITS, LPR, CPL, UB> ta;
-  if (nloc > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, 0, nloc, rs, cl);
+  gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, 0, nloc, rs, cl);
 
   if constexpr (XM == kXNorm) {
     __shared__ float nred[4];
-    stage_x_norm<WBITS>(x, nm, xs, nred, K);
+    norm_pin(nin);
+    stage_x_norm<WBITS>(nin, nm, xs, nred, K);
   } else if constexpr (XM == kXFwht) {
     stage_x_fwht<WBITS>(x, nm.h, nm.split, xs, K);
   } else {
-    stage_x<WBITS>(x, xs, cpr);
+    plain_pin(pin);
+    stage_x(pin, xs, cpr);
   }
   uint32_t xr[CPL * XD];
 #pragma unroll
@@ -571,24 +634,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   float* red = reinterpret_cast<float*>(xs);
   if constexpr (WPR > 1) __syncthreads();
 
-  // At most one step's chunks in flight per lane: with ~3 workgroups per CU
-  // the chip-wide bytes in flight stay near the ~8-16 MB at which HBM
-  // streams best (measured: double-buffering whole steps lowers the
-  // bandwidth), while the rolling refill keeps the stream going during the
-  // arithmetic (measured 11.9 -> 10.4 us for 17408 x 5120 INT4).
-  if constexpr (kRollingPrefetch && UB == 1) {
-    for (int k = 0; k + 1 < nloc; ++k)
+  // Rolling prefetch over a ring of UB steps: step k is computed from slot
+  // k % UB, which then receives step k + UB, so UB steps stay in flight per
+  // lane.  The first UB steps were requested before the activation staging.
+  // One step in flight (UB = 1) is the default: it keeps the chip near the
+  // ~8-16 MB in flight at which HBM streams best.  Measured in the 40-layer
+  // step with the activation loads issued first: 2, 3 and 4 steps in flight
+  // made every projection slower (qkv + norm 8.0 -> 8.2 / 10.2 us, gate_up
+  // 20.2 -> 21.2 / 26.5 us, down 12.6 -> 13.3 / 20.1 us); load-then-compute
+  // batches were slower still (11.9 vs 10.4 us for 17408 x 5120 INT4).
+  // Steady-state blocks of UB steps refill every slot; only the last
+  // 2 UB - 1 steps test for the end.
+  int k0 = 0;
+  for (; k0 + 2 * UB <= nloc; k0 += UB) {
+#pragma unroll
+    for (int j = 0; j < UB; ++j)
       gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, EPI>, EPI, true>(
-          ta, xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, k, rs, cl);
-    if (nloc > 0)
+          ta.wq[j], ta.s2[j], xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, k0 + j,
+          k0 + j + UB, rs, cl);
+  }
+#pragma unroll
+  for (int jj = 0; jj < 2 * UB - 1; ++jj) {
+    const int k = k0 + jj, j = jj % UB;
+    if (k >= nloc) break;  // workgroup-uniform
+    if (k + UB < nloc)
+      gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, EPI>, EPI, true>(
+          ta.wq[j], ta.s2[j], xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, k, k + UB, rs,
+          cl);
+    else
       gemv_step_roll<WBITS, LPR, CPL, RowMap<RPS, EPI>, EPI, false>(
-          ta, xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, nloc - 1, rs, cl);
-  } else {
-    for (int k = 0; k < nloc; k += UB) {
-      if (k > 0) gemv_load(ta, w, sz, row_bytes, nb, cpr, N, map, k, nloc, rs, cl);
-      gemv_compute<WBITS, LPR, CPL, UB, RowMap<RPS, EPI>, EPI>(ta, xr, y, red, ut, cpr, N,
-                                                                map, k, nloc, rs, cl);
-    }
+          ta.wq[j], ta.s2[j], xr, w, sz, row_bytes, nb, y, red, ut, cpr, N, map, k, 0, rs, cl);
   }
   if constexpr (WPR > 1) {
     __syncthreads();
@@ -642,9 +717,15 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
                        : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
   const int wgs_o = tuning().gemv_wgs.load(), ub_o = tuning().gemv_ub.load();
   const int max_wg = wgs_o ? wgs_o : dflt;
-  const int ub = ub_o ? ub_o : 1;
   const int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
   const int64_t grid = (nsteps + per - 1) / per;
+  // steps in flight per lane: at most the steps a workgroup has (a deeper
+  // ring would re-read its last step)
+  const int64_t spw = epi == kEpiSiluUnit   ? (64 / rps) * per
+                      : epi == kEpiSiluPair ? (F > 0 ? 64 / rps : 0) +
+                                                  2 * (((N / 2 - norm->split) / rps + grid - 1) / grid)
+                                            : per;
+  const int ub = (int)std::max<int64_t>(1, std::min<int64_t>(ub_o ? ub_o : 1, spw));
   // the staging area also holds one partial per (step, wave) of the workgroup
   const size_t lds_all = lds > (size_t)per * 16 ? lds : (size_t)per * 16;
   R4Q_REQUIRE(lds_all <= 64 * 1024, "gemv: N=%lld too large for one launch", (long long)N);
@@ -689,7 +770,7 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   R4Q_GEMV(128, 1) R4Q_GEMV(256, 1) R4Q_GEMV(128, 2) R4Q_GEMV(256, 2)
 #undef R4Q_GEMV
 #undef R4Q_GEMV_K
-  return fail(R4Q_EUNSUPPORTED, "gemv: no kernel for %d lanes/row, %d steps/batch", lpr, ub);
+  return fail(R4Q_EUNSUPPORTED, "gemv: no kernel for %d lanes/row, %d steps in flight", lpr, ub);
 }
 
 }  // namespace

@@ -26,7 +26,7 @@ int launch_status(const char* what);
 // its range is ignored (environment) or rejected (r4q_tune).
 //   gemv_lpr      R4Q_GEMV_LPR      lanes per GEMV row: 16, 32, 64, 128, 256
 //   gemv_wgs      R4Q_GEMV_WGS      GEMV workgroup cap: 1 .. 65536
-//   gemv_ub       R4Q_GEMV_UB       GEMV steps per batch: 1 or 2
+//   gemv_ub       R4Q_GEMV_UB       GEMV steps in flight per lane: 1 or 2
 //   attn_splits   R4Q_ATTN_SPLITS   flash-decode splits: 1 .. 128
 //   skinny_splits R4Q_SKINNY_SPLITS skinny-GEMM K splits: 1 .. 8
 //   gemm_splits   R4Q_GEMM_SPLITS   ring-GEMM K splits of every tile: 1 .. 16
