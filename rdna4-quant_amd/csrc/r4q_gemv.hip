@@ -352,37 +352,71 @@ __device__ __forceinline__ void stage_x_norm(const NormIn& in, const GemvNorm& n
 
 // Activation of the down projection after the split SiLU-gate epilogue:
 // elements below `split` are fp16 already (x); above it x = fp16(FWHT32(h))
-// per 32-element chunk from the fp32 products h, with the butterflies,
+// per 32-element piece from the fp32 products h, with the butterflies,
 // scaling and rounding of silu_kernel<true> (fwht32, store32h), so the
-// staged activation is bit-identical to that kernel's output.
-template <int WBITS>
-__device__ __forceinline__ void stage_x_fwht(const uint16_t* __restrict__ x,
-                                             const float* __restrict__ h, int split, uint32_t* xs,
+// staged activation is bit-identical to that kernel's output.  Thread t
+// stages pieces t, t + 256, ... (at most NPF); all of them are requested
+// before the first weight steps (see NormIn): each as 32 dwords, from h
+// for an fp32 piece or from x (its 16 dwords read twice) for an fp16 one,
+// at clamped addresses and without branches.
+template <int WBITS, int LPR, int CPL>
+struct FwhtIn {
+  static constexpr int XD = Fmt<WBITS>::kXDw;
+  static constexpr int kRow = (LPR * CPL * Fmt<WBITS>::kElems / 32 + 255) / 256;
+  static constexpr int kLds =
+      (65536 / (XD * 4) * Fmt<WBITS>::kElems / 32 + 255) / 256;  // pieces the LDS stage holds
+  static constexpr int NPF = kRow < kLds ? kRow : kLds;
+  uint32_t raw[NPF][32];
+};
+
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void fwht_issue(const uint16_t* __restrict__ x,
+                                           const float* __restrict__ h, int split,
+                                           FwhtIn<WBITS, LPR, CPL>& in, int K) {
+#pragma unroll
+  for (int i = 0; i < FwhtIn<WBITS, LPR, CPL>::NPF; ++i) {
+    const int p = min((int)threadIdx.x + 256 * i, K / 32 - 1);
+    const bool half = 32 * p < split;
+    const u4_t* src = half ? reinterpret_cast<const u4_t*>(x + (int64_t)p * 32)
+                           : reinterpret_cast<const u4_t*>(h + (int64_t)p * 32);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const u4_t v = src[half ? (q & 3) : q];
+      in.raw[i][4 * q] = v[0];
+      in.raw[i][4 * q + 1] = v[1];
+      in.raw[i][4 * q + 2] = v[2];
+      in.raw[i][4 * q + 3] = v[3];
+    }
+  }
+}
+
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void fwht_pin(FwhtIn<WBITS, LPR, CPL>& in) {
+#pragma unroll
+  for (int i = 0; i < FwhtIn<WBITS, LPR, CPL>::NPF; ++i)
+#pragma unroll
+    for (int k = 0; k < 32; ++k) asm volatile("" : "+v"(in.raw[i][k])::"memory");
+}
+
+template <int WBITS, int LPR, int CPL>
+__device__ __forceinline__ void stage_x_fwht(FwhtIn<WBITS, LPR, CPL>& in, int split, uint32_t* xs,
                                              int K) {
   constexpr int E = Fmt<WBITS>::kElems;
   constexpr int XD = Fmt<WBITS>::kXDw;
-  for (int c = threadIdx.x; c < K / 32; c += blockDim.x) {
-    if (32 * c < split) {
 #pragma unroll
-      for (int sub = 0; sub < 32 / E; ++sub)
-        prep_chunk<WBITS>(x, c * (32 / E) + sub, xs + (c * (32 / E) + sub) * XD);
-      continue;
+  for (int i = 0; i < FwhtIn<WBITS, LPR, CPL>::NPF; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    if (c >= K / 32) break;
+    uint32_t* raw = in.raw[i];
+    if (32 * c >= split) {
+      float v[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) v[k] = __uint_as_float(raw[k]);
+      fwht32(v);
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        raw[k] = (uint32_t)f2h(v[2 * k]) | ((uint32_t)f2h(v[2 * k + 1]) << 16);
     }
-    const f4_t* src = reinterpret_cast<const f4_t*>(h + (int64_t)c * 32);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f4_t q = src[i];
-      v[4 * i] = q[0];
-      v[4 * i + 1] = q[1];
-      v[4 * i + 2] = q[2];
-      v[4 * i + 3] = q[3];
-    }
-    fwht32(v);
-    uint32_t raw[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      raw[i] = (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
 #pragma unroll
     for (int sub = 0; sub < 32 / E; ++sub)
       prep_raw<WBITS>(raw + sub * (E / 2), xs + (c * (32 / E) + sub) * XD);
@@ -463,18 +497,23 @@ __device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
                                           const uint32_t* __restrict__ sz, int64_t row_bytes,
                                           int nb, int cpr, int N, const Map& map, int k0,
                                           int nloc, int rs, int cl) {
+  // weight chunks, then their (scale, zero) words: the activation staging,
+  // requested before both, waits for neither
+  int rowc[UB];
 #pragma unroll
   for (int j = 0; j < UB; ++j) {
     const int k = max(0, min(k0 + j, nloc - 1));  // clamped: in bounds
-    const int rowc = min(map.row0(k) + rs, N - 1);
-    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes);
-    const uint32_t* srow = sz + (int64_t)rowc * nb;
+    rowc[j] = min(map.row0(k) + rs, N - 1);
+    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc[j] * row_bytes);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = min(cl + LPR * i, cpr - 1);
-      t.wq[j][i] = load_nt(wrow + c);
-      t.s2[j][i] = load_sz<WBITS>(srow, c);
-    }
+    for (int i = 0; i < CPL; ++i) t.wq[j][i] = load_nt(wrow + min(cl + LPR * i, cpr - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < UB; ++j) {
+    const uint32_t* srow = sz + (int64_t)rowc[j] * nb;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) t.s2[j][i] = load_sz<WBITS>(srow, min(cl + LPR * i, cpr - 1));
   }
 }
 
@@ -610,8 +649,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
 
   NormIn nin;
   PlainIn<WBITS, LPR, CPL> pin;
+  FwhtIn<WBITS, LPR, CPL> fin;
   if constexpr (XM == kXNorm) norm_issue(x, nm, nin, K);
   else if constexpr (XM == kXPlain) plain_issue(x, pin, cpr);
+  else fwht_issue(x, nm.h, nm.split, fin, K);
   // the first UB steps (unconditional and clamped, so that the compiler's
   // wait counts stay exact: a workgroup without steps re-reads a valid row)
   GemvTile<WBITS, LPR, CPL, UB> ta;
@@ -622,7 +663,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
     norm_pin(nin);
     stage_x_norm<WBITS>(nin, nm, xs, nred, K);
   } else if constexpr (XM == kXFwht) {
-    stage_x_fwht<WBITS>(x, nm.h, nm.split, xs, K);
+    fwht_pin(fin);
+    stage_x_fwht(fin, nm.split, xs, K);
   } else {
     plain_pin(pin);
     stage_x(pin, xs, cpr);
