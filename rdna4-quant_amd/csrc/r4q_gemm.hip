@@ -227,19 +227,22 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 // the raw weight bytes (plus the (scale, zero) words) of a K step land in
 // LDS by direct global->LDS copies (global_load_lds_dwordx4 / _dword) in a
 // ring of Ring::kStages stages, so that several steps are in flight while
-// one is multiplied, without holding them in VGPRs.  The workgroup
-// dequantises the weights of step i+1 (16 elements per thread, natural
-// element order, bit-identical to r4q_dequant_int4/8) into one of two fp16
-// B tiles while step i is multiplied from the other.
-// X rows are 64 bytes per step; the 16-byte piece p of row r sits in LDS
-// slot p ^ ((r >> 1) & 3) of the row, which spreads the fragment reads of
-// consecutive rows over the banks (measured: half the bank conflicts of
-// p ^ ((r >> 2) & 3)).  B tile rows are padded to 80 bytes.
+// one is multiplied, without holding them in VGPRs.
+// Each wave dequantises its own B fragments straight from the raw bytes in
+// LDS into registers (one 4-byte INT4 / 8-byte INT8 read per fragment
+// instead of 16 bytes of fp16), one step ahead, interleaved with the MFMAs
+// of the current step; the fp16 values equal r4q_dequant_int4/8 bit for bit.
+// LDS layouts are bank-conflict-free for their fragment reads (measured on
+// MI355X with a read-throughput probe):
+//  * X rows are 64 bytes per step; the 16-byte piece p of row r sits in slot
+//    p ^ ((r >> 1) & 3) of the row;
+//  * INT4 weight rows are 16 bytes per step; dword d of row r sits in slot
+//    d ^ (((r >> 3) & 1) << 1) (rows 8 apart would share banks otherwise);
+//  * INT8 weight rows are 32 bytes per step (two 16-byte pieces, unswizzled).
 // One barrier per K step i: before it each wave waits for its own copies of
-// step i+1; after it every wave's copies are visible, the B tile of step i
-// is complete, and every wave is done with step i-1, whose ring slot then
-// receives step i+kStages-1 and whose B tile receives step i+1.  Every wave
-// issues the same number of copies per stage (the wait counts are per
+// step i+1; after it every wave's copies are visible and every wave is done
+// with step i-1, whose ring slot then receives step i+kStages-1.  Every
+// wave issues the same number of copies per stage (the wait counts are per
 // wave): the scale words take one copy of waves 0-3, and waves 4-7 repeat
 // theirs into a spare area.
 // Work split (1-D grid, tiles numbered M-tile-major): blocks 0 .. full-1
@@ -252,16 +255,14 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 // the last round's tiles are, so that round keeps every CU busy.
 constexpr int RBM = 256, RBN = 256, RBK = 32;
 constexpr int kRingThreads = 512;
-constexpr int kBRow = 40;  // halves per B tile row (32 + 8 pad)
 
 template <int WBITS>
 struct Ring {
-  static constexpr int kStages = WBITS == 4 ? 5 : 4;
+  static constexpr int kStages = WBITS == 4 ? 6 : 5;
   static constexpr int kX = RBM * RBK * 2;          // X: 16 KB
   static constexpr int kW = RBN * RBK * WBITS / 8;  // raw weights: 4 KB (INT4) / 8 KB (INT8)
   static constexpr int kS = RBN * 4;                // (scale, zero) per row
   static constexpr int kStage = kX + kW + 2 * kS;   // + spare area for waves 4-7
-  static constexpr int kB = RBN * kBRow * 2;        // one fp16 B tile: 20 KB
   static constexpr int kPerStage = 2 + (WBITS == 4 ? 2 : 1) + 1;  // copies per wave per stage
 };
 
@@ -308,9 +309,10 @@ __device__ __forceinline__ void ring_issue(uint8_t* stage, const uint16_t* __res
   if constexpr (WBITS == 4) {  // 16 bytes per row: 2 copies of 16 rows x 4 dwords
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int r0 = 32 * wave + 16 * q;
+      const int r0 = 32 * wave + 16 * q;  // a multiple of 16: row bit 3 is lane bit 5
       const int64_t n = min(n0 + r0 + (lane >> 2), N - 1);
-      copy4(W + n * (K / 2) + kb * 16 + 4 * (lane & 3), wst + r0 * 16);
+      const int d = (lane & 3) ^ (((lane >> 5) & 1) << 1);  // dword held by slot lane & 3
+      copy4(W + n * (K / 2) + kb * 16 + 4 * d, wst + r0 * 16);
     }
   } else {  // 32 bytes per row: 32 rows x 2 pieces of 16 bytes
     const int r0 = 32 * wave;
@@ -324,44 +326,67 @@ __device__ __forceinline__ void ring_issue(uint8_t* stage, const uint16_t* __res
   }
 }
 
-// Dequantises half a weight row of one ring stage (16 elements: row t / 2,
-// elements 16 (t % 2) ..) into the fp16 B tile: fp16((q - zp) * scale) as
-// (1024 + q) - (1024 + zp) (exact) times scale (one rounding).
+// B fragments of one ring stage for a wave: fragment j is column c of the
+// wave's 16-column block j (weight row wn + 16 j + c) at k labels
+// 8 g .. 8 g + 7, dequantised to fp16 as fp16((q - zp) * scale) computed as
+// ((1024 + q) - (1024 + zp)) * scale in fp16 pairs (the difference is exact,
+// one rounding in the product).  The raw reads are issued first (frag_load),
+// the arithmetic later (frag_dequant), so that it can interleave with MFMAs.
 template <int WBITS>
-__device__ __forceinline__ void ring_dequant(const uint8_t* stage, uint16_t* bt, int t) {
+struct BRaw {
+  uint32_t w[4][WBITS == 4 ? 1 : 2];
+  uint32_t s2[4];
+};
+
+template <int WBITS>
+__device__ __forceinline__ void frag_load(const uint8_t* stage, BRaw<WBITS>& r, int wn, int c,
+                                          int g) {
   using R = Ring<WBITS>;
-  const int row = t >> 1, half = t & 1;
-  const uint32_t s2 = *reinterpret_cast<const uint32_t*>(stage + R::kX + R::kW + row * 4);
-  const uint32_t sb = s2 & 0xFFFFu, zb = s2 >> 16;
-  const h2_t sc = as_h2(sb | (sb << 16));
-  const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
-  uint32_t pr[8];  // (1024 + q_2k, 1024 + q_2k+1) as fp16 pairs
-  if constexpr (WBITS == 4) {
-    const u2_t w = *reinterpret_cast<const u2_t*>(stage + R::kX + row * 16 + 8 * half);
-    typedef uint16_t us2 __attribute__((ext_vector_type(2)));
-    const us2 sh = {0, 4};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t wd = w[k >> 2], b = k & 3;
-      // byte b in both halves, the high half shifted down by 4: (lo nibble, hi nibble)
-      const uint32_t tb = __builtin_amdgcn_perm(0u, wd, (b | 0x0C00u | (b << 16) | 0x0C000000u));
-      const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
-      pr[k] = (nib & 0x000F000Fu) | 0x64006400u;
+  for (int j = 0; j < 4; ++j) {
+    const int row = wn + 16 * j + c;
+    if constexpr (WBITS == 4) {
+      r.w[j][0] = *reinterpret_cast<const uint32_t*>(stage + R::kX + row * 16 +
+                                                     4 * (g ^ (((c >> 3) & 1) << 1)));
+    } else {
+      const u2_t v = *reinterpret_cast<const u2_t*>(stage + R::kX + row * 32 + 8 * g);
+      r.w[j][0] = v[0];
+      r.w[j][1] = v[1];
     }
-  } else {
-    const u4_t w = *reinterpret_cast<const u4_t*>(stage + R::kX + row * 32 + 16 * half);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t wd = w[k >> 1];
-      pr[k] = __builtin_amdgcn_perm(wd, 0x64646464u, (k & 1) ? 0x00070006u : 0x00050004u);
-    }
+    r.s2[j] = *reinterpret_cast<const uint32_t*>(stage + R::kX + R::kW + row * 4);
   }
-  u4_t o[2];
+}
+
+template <int WBITS>
+__device__ __forceinline__ void frag_dequant(const BRaw<WBITS>& r, h8_t* bf) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) o[k >> 2][k & 3] = as_u32((as_h2(pr[k]) + nz) * sc);
-  u4_t* dst = reinterpret_cast<u4_t*>(bt + row * kBRow + 16 * half);
-  dst[0] = o[0];
-  dst[1] = o[1];
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t sb = r.s2[j] & 0xFFFFu, zb = r.s2[j] >> 16;
+    const h2_t sc = as_h2(sb | (sb << 16));
+    const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
+    uint32_t pr[4];  // (1024 + q_2k, 1024 + q_2k+1) as fp16 pairs
+    if constexpr (WBITS == 4) {
+      typedef uint16_t us2 __attribute__((ext_vector_type(2)));
+      const us2 sh = {0, 4};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // byte k in both halves, the high half shifted down by 4
+        const uint32_t tb =
+            __builtin_amdgcn_perm(0u, r.w[j][0], (k | 0x0C00u | (k << 16) | 0x0C000000u));
+        const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
+        pr[k] = (nib & 0x000F000Fu) | 0x64006400u;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        pr[k] = __builtin_amdgcn_perm(r.w[j][k >> 1], 0x64646464u,
+                                      (k & 1) ? 0x00070006u : 0x00050004u);
+    }
+    u4_t o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = as_u32((as_h2(pr[k]) + nz) * sc);
+    bf[j] = __builtin_bit_cast(h8_t, o);
+  }
 }
 
 template <int N>
@@ -384,7 +409,6 @@ __global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
   using R = Ring<WBITS>;
   constexpr int S = R::kStages;
   __shared__ __align__(16) uint8_t ring[S * R::kStage];
-  __shared__ __align__(16) uint16_t btile[2][RBN * kBRow];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int b = blockIdx.x;
   const bool split = b >= full;  // workgroup-uniform
@@ -409,7 +433,6 @@ __global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
     const int row = wm + 16 * i + c;
     xoff[i] = row * 64 + 16 * (g ^ ((row >> 1) & 3));
   }
-  const int boff = (wn + c) * kBRow + 8 * g;
 
   // stages past the split's end repeat its last step (same copy counts in
   // every iteration; their data is never multiplied)
@@ -419,35 +442,46 @@ __global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
                       lane);
   wait_copies<(S - 2) * R::kPerStage>();  // step 0
   ring_barrier();
-  ring_dequant<WBITS>(ring, btile[0], t);
-  for (int i = 0; i < nk; ++i) {
+  // Two register sets (A fragments and dequantised B fragments) alternate
+  // between even and odd steps, so that no step overwrites registers the
+  // previous step's MFMAs may still be reading.
+  h8_t bf0[4], bf1[4];
+  {
+    BRaw<WBITS> r0;
+    frag_load<WBITS>(ring, r0, wn, c, g);
+    frag_dequant<WBITS>(r0, bf0);
+  }
+  auto kstep = [&](int i, h8_t (&bf)[4], h8_t (&bn)[4]) {
     wait_copies<(S - 3) * R::kPerStage>();  // this wave's copies of step i+1 landed
     ring_barrier();
     ring_issue<WBITS>(ring + ((i + S - 1) % S) * R::kStage, X, W, SZ, M, N, K, m0, n0,
                       kb0 + min(i + S - 1, nk - 1), wave, lane);
     const uint8_t* st = ring + (i % S) * R::kStage;
-    const uint16_t* bt = btile[i & 1];
-    h8_t bf[4], af[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = *reinterpret_cast<const h8_t*>(bt + boff + 16 * j * kBRow);
+    h8_t af[8];
 #pragma unroll
     for (int i8 = 0; i8 < 8; ++i8) af[i8] = *reinterpret_cast<const h8_t*>(st + xoff[i8]);
+    // step i+1's B fragments (raw reads now, dequantised between the MFMAs)
+    BRaw<WBITS> rn;
+    frag_load<WBITS>(ring + ((i + 1) % S) * R::kStage, rn, wn, c, g);
 #pragma unroll
     for (int i8 = 0; i8 < 8; ++i8)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i8][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i8], bf[j], acc[i8][j], 0, 0, 0);
-    // step i+1's weights dequantised while step i's MFMAs run: LDS reads
-    // first, then one MFMA per two VALU instructions, the B tile writes last
-    ring_dequant<WBITS>(ring + ((i + 1) % S) * R::kStage, btile[(i + 1) & 1], t);
+    frag_dequant<WBITS>(rn, bn);
     __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
     }
-    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);  // DS writes
+  };
+  int i = 0;
+  for (; i + 1 < nk; i += 2) {
+    kstep(i, bf0, bf1);
+    kstep(i + 1, bf1, bf0);
   }
+  if (i < nk) kstep(i, bf0, bf1);
   wait_copies<0>();  // no copy may land after the workgroup's LDS is released
   // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block
 #pragma unroll
