@@ -458,6 +458,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the config-3 prefill GEMM leg (the program the MFMA "
                          "counter runs profile)")
+    ap.add_argument("--flash-only", action="store_true",
+                    help="run only the config-2 flash-decode leg (the program the "
+                         "flash-decode kernel trace profiles)")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the config-4 decode leg (the program the decode kernel "
                          "trace profiles)")
@@ -476,6 +479,14 @@ def main():
     dev = torch.device("cuda:0")
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": prefill_gemm_leg(dev)}), flush=True)
+        return
+    if args.flash_only:
+        out = {}
+        for c in (128, 2048, 8192, 32768):
+            a_us, a_bytes = flash_decode_leg(dev, c)
+            out[str(c)] = {"us": round(a_us, 3), "kv_bytes": a_bytes,
+                           "gbps": round(a_bytes / a_us / 1e3, 1)}
+        print(json.dumps({"flash_decode": out}), flush=True)
         return
     if args.roofline_only:
         us, alg = gemv_roofline(dev, eager_tail=2 * 8)

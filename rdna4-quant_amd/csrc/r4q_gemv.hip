@@ -497,23 +497,20 @@ __device__ __forceinline__ void gemv_load(GemvTile<WBITS, LPR, CPL, UB>& t,
                                           const uint32_t* __restrict__ sz, int64_t row_bytes,
                                           int nb, int cpr, int N, const Map& map, int k0,
                                           int nloc, int rs, int cl) {
-  // weight chunks, then their (scale, zero) words: the activation staging,
-  // requested before both, waits for neither
-  int rowc[UB];
+  // each weight chunk with its (scale, zero) word, so that the first chunks'
+  // arithmetic can start while the rest of the step is in flight
 #pragma unroll
   for (int j = 0; j < UB; ++j) {
     const int k = max(0, min(k0 + j, nloc - 1));  // clamped: in bounds
-    rowc[j] = min(map.row0(k) + rs, N - 1);
-    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc[j] * row_bytes);
+    const int rowc = min(map.row0(k) + rs, N - 1);
+    const u4_t* wrow = reinterpret_cast<const u4_t*>(w + (int64_t)rowc * row_bytes);
+    const uint32_t* srow = sz + (int64_t)rowc * nb;
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) t.wq[j][i] = load_nt(wrow + min(cl + LPR * i, cpr - 1));
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < UB; ++j) {
-    const uint32_t* srow = sz + (int64_t)rowc[j] * nb;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) t.s2[j][i] = load_sz<WBITS>(srow, min(cl + LPR * i, cpr - 1));
+    for (int i = 0; i < CPL; ++i) {
+      const int c = min(cl + LPR * i, cpr - 1);
+      t.wq[j][i] = load_nt(wrow + c);
+      t.s2[j][i] = load_sz<WBITS>(srow, c);
+    }
   }
 }
 
