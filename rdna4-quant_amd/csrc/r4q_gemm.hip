@@ -9,9 +9,10 @@
 //
 // Three kernels, by shape:
 //  * gemm_ring_kernel (M >= 256, INT4 / INT8): 256 x 256 tiles, X and the
-//    raw weights copied global -> LDS through a multi-stage ring, the
-//    weights dequantised once per workgroup into an fp16 B tile, optional
-//    deterministic split-K over a caller workspace (see its comment);
+//    raw weights copied global -> LDS through a ring, the weights
+//    dequantised per wave in registers, the K units of the tiles shared
+//    evenly by the CUs (stream-K, deterministic reduce over a caller
+//    workspace; see its comment);
 //  * gemm_mfma_kernel (17 <= M < 256, and FP16 weights): 128 x 128 tiles,
 //    X and the dequantised W staged in LDS per 32-wide K step;
 //  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows
@@ -228,42 +229,61 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 // LDS by direct global->LDS copies (global_load_lds_dwordx4 / _dword) in a
 // ring of Ring::kStages stages, so that several steps are in flight while
 // one is multiplied, without holding them in VGPRs.
+// X of a K step (16 KB) lands in LDS by direct global->LDS copies
+// (global_load_lds_dwordx4) in a ring of kXStages stages; the raw weights
+// and their (scale, zero) words arrive per super-step of Ring::KS K steps
+// (128 bytes of each weight row: whole cache lines, where one step's 16 / 32
+// bytes of 256 rows would touch 256 lines per step) into two alternating
+// buffers, requested a super-step ahead.
 // Each wave dequantises its own B fragments straight from the raw bytes in
 // LDS into registers (one 4-byte INT4 / 8-byte INT8 read per fragment
 // instead of 16 bytes of fp16), one step ahead, interleaved with the MFMAs
 // of the current step; the fp16 values equal r4q_dequant_int4/8 bit for bit.
+// X fragments 0-3 of a step are read during the previous step's MFMAs, so
+// that each step starts its MFMAs without waiting for LDS.
 // LDS layouts are bank-conflict-free for their fragment reads (measured on
 // MI355X with a read-throughput probe):
 //  * X rows are 64 bytes per step; the 16-byte piece p of row r sits in slot
 //    p ^ ((r >> 1) & 3) of the row;
-//  * INT4 weight rows are 16 bytes per step; dword d of row r sits in slot
-//    d ^ (((r >> 3) & 1) << 1) (rows 8 apart would share banks otherwise);
-//  * INT8 weight rows are 32 bytes per step (two 16-byte pieces, unswizzled).
+//  * weight rows are 128 bytes per super-step; chunk q (16 bytes) of row r
+//    sits in slot q ^ wswz(r);
+//  * scale words are in natural order (rows 8 apart share a bank: a 2-way
+//    conflict on 4 of the 12 reads per step).
 // One barrier per K step i: before it each wave waits for its own copies of
 // step i+1; after it every wave's copies are visible and every wave is done
-// with step i-1, whose ring slot then receives step i+kStages-1.  Every
-// wave issues the same number of copies per stage (the wait counts are per
-// wave): the scale words take one copy of waves 0-3, and waves 4-7 repeat
-// theirs into a spare area.
-// Work split (1-D grid, tiles numbered M-tile-major): blocks 0 .. full-1
-// each compute a whole tile and write fp16; the remaining nst tiles are
-// split S ways along K -- block full + S j + s covers K steps
-// [s*kps, (s+1)*kps) of tile full + j and writes its fp32 partial to
-// part[s][j] (256 x 256) -- and gemm_splitk_reduce_kernel sums the S
-// partials of each split tile in split order (deterministic).  With
-// full = 0 every tile is split; with full a multiple of the CU count only
-// the last round's tiles are, so that round keeps every CU busy.
+// with step i-1, whose X stage then receives step i+kXStages-1.  Every
+// wave issues the same number of copies per step position (the wait counts
+// are per wave).
+// Work split: tiles of 256 x 256 outputs, each a K loop of U units (one
+// unit = one weight super-step, below).  Blocks [0, dp) compute tiles
+// 0 .. dp-1 whole.  The sk stream-K workgroups share the units of tiles
+// dp .. T-1 evenly: workgroup w takes the flattened units
+// [floor(w * TU / sk), floor((w + 1) * TU / sk)) (TU = (T - dp) * U), i.e. the
+// tail of one tile, whole tiles, the head of another.  A tile done by one
+// workgroup is written as fp16 directly; a tile shared by several writes one
+// fp32 partial per workgroup (segment j = w - the first workgroup on the
+// tile) and gemm_splitk_reduce_kernel sums them in segment order, so the
+// result does not depend on timing.
 constexpr int RBM = 256, RBN = 256, RBK = 32;
-constexpr int kRingThreads = 512;
+constexpr int kRingWaves = 4;  // one per SIMD; wave w owns output columns 64w .. 64w+63
+constexpr int kRingThreads = 64 * kRingWaves;
+constexpr int kRingRows = RBM / kRingWaves;  // rows of X / W each wave copies
+constexpr int kXStages = 4;                   // X ring depth (one K step per stage)
 
 template <int WBITS>
 struct Ring {
-  static constexpr int kStages = WBITS == 4 ? 6 : 5;
-  static constexpr int kX = RBM * RBK * 2;          // X: 16 KB
-  static constexpr int kW = RBN * RBK * WBITS / 8;  // raw weights: 4 KB (INT4) / 8 KB (INT8)
-  static constexpr int kS = RBN * 4;                // (scale, zero) per row
-  static constexpr int kStage = kX + kW + 2 * kS;   // + spare area for waves 4-7
-  static constexpr int kPerStage = 2 + (WBITS == 4 ? 2 : 1) + 1;  // copies per wave per stage
+  // K steps per weight super-step: 128 bytes of every weight row, fetched
+  // as whole cache lines (INT4: 8 steps of 16 bytes, INT8: 4 of 32)
+  static constexpr int KS = WBITS == 4 ? 8 : 4;
+  static constexpr int kX = RBM * RBK * 2;    // one X stage: 16 KB
+  static constexpr int kW = RBN * 128;        // one super-step of raw weights: 32 KB
+  static constexpr int kS = RBN * KS * 4;     // its (scale, zero) words: 8 KB / 4 KB
+  static constexpr int kWOff = kXStages * kX;  // two weight buffers follow the X stages
+  static constexpr int kSOff = kWOff + 2 * kW;
+  static constexpr int kBytes = kSOff + 2 * kS;  // 144 KB / 136 KB
+  static constexpr int kXCopies = kRingRows / 16;  // copies per wave per X stage
+  // per wave per super-step: weights (8 rows per copy), scale words
+  static constexpr int kWCopies = kRingRows / 8 + kRingRows * KS / 64;
 };
 
 // Global -> LDS copy of 16 (4) bytes per lane: lane l's bytes land at
@@ -285,48 +305,90 @@ __device__ __forceinline__ void copy4(const void* g, void* lds) {
                "v"(g)
                : "memory");
 }
+// LDS-qualified byte pointer: ring addresses stay 32-bit LDS offsets (a
+// generic pointer into LDS is a 64-bit value the compiler keeps in VGPRs).
+typedef __attribute__((address_space(3))) uint8_t lds8;
+template <class T>
+__device__ __forceinline__ T lds_ld(const lds8* p) {
+  return *(const __attribute__((address_space(3))) T*)p;
+}
+__device__ __forceinline__ uint32_t lds_off(const lds8* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
 
-// Copies K step kb (32 elements) of the workgroup's 256 X rows and 256
-// weight rows into one ring stage; every source row is clamped into the
-// matrix (rows past M / N are computed and not stored).  Wave w copies X
-// rows 32w .. 32w+31 (2 copies of 16 rows x 64 bytes) and weight rows
-// 32w .. 32w+31.
-template <int WBITS>
-__device__ __forceinline__ void ring_issue(uint8_t* stage, const uint16_t* __restrict__ X,
-                                           const uint8_t* __restrict__ W,
-                                           const uint32_t* __restrict__ SZ, int M, int N, int K,
-                                           int m0, int n0, int kb, int wave, int lane) {
-  using R = Ring<WBITS>;
+// The same with a uniform 64-bit base in SGPRs and a 32-bit byte offset
+// per lane (half the VGPRs of a per-lane address).
+__device__ __forceinline__ void copy16s(const void* base, uint32_t off, lds8* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_off(lds)),
+               "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void copy4s(const void* base, uint32_t off, lds8* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_off(lds)),
+               "v"(off), "s"(base)
+               : "memory");
+}
+
+// X of K step kb (32 elements) of the workgroup's 256 rows into one X stage;
+// rows past M are clamped into the matrix (computed, never stored).  Wave w
+// copies rows kRingRows w .. (16 rows x 64 bytes per copy); the 16-byte
+// pieces of a row are XOR-swizzled by (row >> 1) & 3 so that the fragment
+// reads are free of bank conflicts.
+__device__ __forceinline__ void x_issue(lds8* xs, const uint16_t* __restrict__ X, int M, int K,
+                                        int m0, int kb, int wave, int lane) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int r0 = 32 * wave + 16 * q;  // first row of this copy
+  for (int q = 0; q < kRingRows / 16; ++q) {
+    const int r0 = kRingRows * wave + 16 * q;  // first row of this copy
     const int row = r0 + (lane >> 2);
     const int p = (lane & 3) ^ ((row >> 1) & 3);  // global piece held by LDS slot lane & 3
     const int m = min(m0 + row, M - 1);
-    copy16(X + (int64_t)m * K + kb * RBK + 8 * p, stage + r0 * 64);
-  }
-  uint8_t* wst = stage + R::kX;
-  if constexpr (WBITS == 4) {  // 16 bytes per row: 2 copies of 16 rows x 4 dwords
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int r0 = 32 * wave + 16 * q;  // a multiple of 16: row bit 3 is lane bit 5
-      const int64_t n = min(n0 + r0 + (lane >> 2), N - 1);
-      const int d = (lane & 3) ^ (((lane >> 5) & 1) << 1);  // dword held by slot lane & 3
-      copy4(W + n * (K / 2) + kb * 16 + 4 * d, wst + r0 * 16);
-    }
-  } else {  // 32 bytes per row: 32 rows x 2 pieces of 16 bytes
-    const int r0 = 32 * wave;
-    const int64_t n = min(n0 + r0 + (lane >> 1), N - 1);
-    copy16(W + n * K + kb * 32 + 16 * (lane & 1), wst + r0 * 32);
-  }
-  {  // scale words: waves 0-3 rows 64w .. 64w+63; waves 4-7 repeat into the spare area
-    const int r0 = 64 * (wave & 3);
-    const int64_t n = min(n0 + r0 + lane, N - 1);
-    copy4(SZ + n * (K / 32) + kb, stage + R::kX + R::kW + (wave >> 2) * R::kS + r0 * 4);
+    copy16s(X, 2u * ((uint32_t)m * K + kb * RBK + 8 * p), xs + r0 * 64);
   }
 }
 
-// B fragments of one ring stage for a wave: fragment j is column c of the
+// 16-byte chunk swizzle of weight row r in a super-step buffer (128 bytes
+// per row): chunk q of the row sits at slot q ^ wswz(r).  With it the 16
+// rows a fragment read touches (rows c = 0 .. 15 of a 16-row block, each
+// lane group g reading dword g of its chunk) fall on 64 different banks.
+__device__ __forceinline__ int wswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Weights and (scale, zero) words of the super-step starting at K step kb
+// for the workgroup's 256 weight rows (rows past N clamped into the matrix,
+// steps past K clamped to its last step: their data is never multiplied).
+// Weights: wave w copies rows kRingRows w .., 8 rows x 128 bytes per copy
+// (whole cache lines).  Scale words in natural order: INT4 8 per row (32
+// bytes), INT8 4 per row (16 bytes).  Byte offsets fit 32 bits (checked by
+// the host).
+template <int WBITS>
+__device__ __forceinline__ void w_issue(lds8* wb, lds8* sb, const uint8_t* __restrict__ W,
+                                        const uint32_t* __restrict__ SZ, int N, int K, int n0,
+                                        int kb, int wave, int lane) {
+  const int nks = K / RBK;
+  const uint32_t ksz = K / 32;  // scale words per row
+#pragma unroll
+  for (int q = 0; q < kRingRows / 8; ++q) {
+    const int r0 = kRingRows * wave + 8 * q;
+    const int r = r0 + (lane >> 3);
+    const int qg = (lane & 7) ^ wswz(r);  // chunk of the row this lane fetches
+    const uint32_t n = min(n0 + r, N - 1);
+    uint32_t off;
+    if constexpr (WBITS == 4)
+      off = n * (uint32_t)(K / 2) + (uint32_t)min(kb + qg, nks - 1) * 16u;
+    else
+      off = n * (uint32_t)K + (uint32_t)min(kb + (qg >> 1), nks - 1) * 32u + 16u * (qg & 1);
+    copy16s(W, off, wb + r0 * 128);
+  }
+  constexpr int WPR = WBITS == 4 ? 8 : 4;   // scale words per row and super-step
+  constexpr int RPC = 64 / WPR;             // rows per copy
+#pragma unroll
+  for (int q = 0; q < kRingRows / RPC; ++q) {
+    const int r0 = kRingRows * wave + RPC * q;
+    const uint32_t n = min(n0 + r0 + lane / WPR, N - 1);
+    copy4s(SZ, 4u * (n * ksz + (uint32_t)min(kb + lane % WPR, nks - 1)), sb + r0 * WPR * 4);
+  }
+}
+
+// B fragments of one K step for a wave: fragment j is column c of the
 // wave's 16-column block j (weight row wn + 16 j + c) at k labels
 // 8 g .. 8 g + 7, dequantised to fp16 as fp16((q - zp) * scale) computed as
 // ((1024 + q) - (1024 + zp)) * scale in fp16 pairs (the difference is exact,
@@ -337,25 +399,6 @@ struct BRaw {
   uint32_t w[4][WBITS == 4 ? 1 : 2];
   uint32_t s2[4];
 };
-
-template <int WBITS>
-__device__ __forceinline__ void frag_load(const uint8_t* stage, BRaw<WBITS>& r, int wn, int c,
-                                          int g) {
-  using R = Ring<WBITS>;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = wn + 16 * j + c;
-    if constexpr (WBITS == 4) {
-      r.w[j][0] = *reinterpret_cast<const uint32_t*>(stage + R::kX + row * 16 +
-                                                     4 * (g ^ (((c >> 3) & 1) << 1)));
-    } else {
-      const u2_t v = *reinterpret_cast<const u2_t*>(stage + R::kX + row * 32 + 8 * g);
-      r.w[j][0] = v[0];
-      r.w[j][1] = v[1];
-    }
-    r.s2[j] = *reinterpret_cast<const uint32_t*>(stage + R::kX + R::kW + row * 4);
-  }
-}
 
 template <int WBITS>
 __device__ __forceinline__ void frag_dequant(const BRaw<WBITS>& r, h8_t* bf) {
@@ -389,6 +432,32 @@ __device__ __forceinline__ void frag_dequant(const BRaw<WBITS>& r, h8_t* bf) {
   }
 }
 
+// Pair k (k labels 8g + 2k, 8g + 2k + 1) of B fragment j, the same
+// arithmetic as frag_dequant, so that the dequantisation can be spread over
+// a step's MFMAs one pair at a time.  nz / sc: fragment j's -(1024 + zp)
+// and scale pairs (set by the pair-0 call).
+template <int WBITS>
+__device__ __forceinline__ uint32_t dq_pair(const BRaw<WBITS>& r, int j, int k, h2_t& nz,
+                                            h2_t& sc) {
+  if (k == 0) {
+    const uint32_t sb = r.s2[j] & 0xFFFFu, zb = r.s2[j] >> 16;
+    sc = as_h2(sb | (sb << 16));
+    nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
+  }
+  uint32_t pr;
+  if constexpr (WBITS == 4) {
+    typedef uint16_t us2 __attribute__((ext_vector_type(2)));
+    const us2 sh = {0, 4};
+    const uint32_t tb =
+        __builtin_amdgcn_perm(0u, r.w[j][0], (k | 0x0C00u | (k << 16) | 0x0C000000u));
+    const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
+    pr = (nib & 0x000F000Fu) | 0x64006400u;
+  } else {
+    pr = __builtin_amdgcn_perm(r.w[j][k >> 1], 0x64646464u, (k & 1) ? 0x00070006u : 0x00050004u);
+  }
+  return as_u32((as_h2(pr) + nz) * sc);
+}
+
 template <int N>
 __device__ __forceinline__ void wait_copies() {  // at most N of this wave's copies outstanding
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -401,121 +470,291 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Stream-K bookkeeping shared by the GEMM and the reduce: first unit of
+// workgroup w, and the workgroup holding unit u.
+__device__ __forceinline__ int64_t sk_lo(int w, int64_t TU, int sk) {
+  return (int64_t)w * TU / sk;
+}
+__device__ __forceinline__ int sk_owner(int64_t u, int64_t TU, int sk) {
+  int w = (int)(u * sk / TU);
+  while (w + 1 < sk && sk_lo(w + 1, TU, sk) <= u) ++w;
+  while (w > 0 && sk_lo(w, TU, sk) > u) --w;
+  return w;
+}
+
+// One segment of a tile: K steps [kb0, kb0 + nk) (kb0 a multiple of KS) of
+// the 256 x 256 tile at (m0, n0), accumulated into acc.  Wave w computes
+// all 256 rows x columns 64w .. 64w+63: 16 x 4 MFMA tiles, 256 fp32
+// accumulators per lane, so that each weight column is dequantised once per
+// workgroup.  Per step the workgroup waits for its copies of the next step,
+// passes one barrier and issues the copies of step + kXStages - 1 (and, at a
+// super-step's first step, the weights of the super-step after next); each
+// wave then requests the raw B fragments of step + 2 and walks its 16 X
+// fragments: 4 MFMAs each, after which the fragment register is refilled
+// with the next step's fragment (so every read has a step of MFMAs to land),
+// with the next step's B dequantised in between.
+// Copies retire in issue order, so one count per step position covers the
+// weights as well: they were issued before the X stage being waited for.
 template <int WBITS>
-__global__ __launch_bounds__(kRingThreads) void gemm_ring_kernel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, float* __restrict__ part, int M,
-    int N, int K, int full, int nsplit, int kps) {
+struct RingSeg {
   using R = Ring<WBITS>;
-  constexpr int S = R::kStages;
-  __shared__ __align__(16) uint8_t ring[S * R::kStage];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int b = blockIdx.x;
-  const bool split = b >= full;  // workgroup-uniform
-  const int slot = split ? (b - full) / nsplit : 0, sp = split ? (b - full) % nsplit : 0;
-  const int tile = split ? full + slot : b, ntn = (N + RBN - 1) / RBN;
-  const int n0 = (tile % ntn) * RBN, m0 = (tile / ntn) * RBM;
-  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
-  const int c = lane & 15, g = lane >> 4;
-  const int kb0 = split ? sp * kps : 0;
-  const int nk = split ? min(K / RBK - kb0, kps) : K / RBK;  // K steps of this block (>= 1)
-  const int nst = (int)(gridDim.x - full) / nsplit;  // split tiles
+  static constexpr int KS = R::KS;
+  lds8* ring;
+  const uint16_t* X;
+  const uint8_t* W;
+  const uint32_t* SZ;
+  int M, N, K, m0, n0, kb0, nk, wave, lane, wn, c, g, hc, xoff;
 
-  f4_t acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  // copies issued after those of X step i+1 when step i waits: the X
+  // stages of the steps in between, and a super-step's weights when step
+  // i-1 began one (position 1)
+  static constexpr int kAfter = R::kXCopies * (kXStages - 3);
 
-  int xoff[8];  // per-lane fragment offsets
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = wm + 16 * i + c;
-    xoff[i] = row * 64 + 16 * (g ^ ((row >> 1) & 3));
+  __device__ __forceinline__ lds8* xst(int i) const { return ring + (i % kXStages) * R::kX; }
+  __device__ __forceinline__ lds8* wbuf(int s) const { return ring + R::kWOff + (s & 1) * R::kW; }
+  __device__ __forceinline__ lds8* sbuf(int s) const { return ring + R::kSOff + (s & 1) * R::kS; }
+
+  __device__ __forceinline__ void issue_x(int i) {
+    x_issue(xst(i), X, M, K, m0, kb0 + min(i, nk - 1), wave, lane);
+  }
+  __device__ __forceinline__ void issue_w(int s) {
+    w_issue<WBITS>(wbuf(s), sbuf(s), W, SZ, N, K, n0, kb0 + s * KS, wave, lane);
   }
 
-  // stages past the split's end repeat its last step (same copy counts in
-  // every iteration; their data is never multiplied)
+  // B fragments of step i (raw reads): position i % KS of super-step i / KS
+  __device__ __forceinline__ void load_b(int i, BRaw<WBITS>& r) const {
+    const int s = i / KS, pos = i % KS;
+    const lds8* wb = wbuf(s);
+    const lds8* sb = sbuf(s) + 4 * pos;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    ring_issue<WBITS>(ring + s * R::kStage, X, W, SZ, M, N, K, m0, n0, kb0 + min(s, nk - 1), wave,
-                      lane);
-  wait_copies<(S - 2) * R::kPerStage>();  // step 0
-  ring_barrier();
-  // Two register sets (A fragments and dequantised B fragments) alternate
-  // between even and odd steps, so that no step overwrites registers the
-  // previous step's MFMAs may still be reading.
-  h8_t bf0[4], bf1[4];
-  {
-    BRaw<WBITS> r0;
-    frag_load<WBITS>(ring, r0, wn, c, g);
-    frag_dequant<WBITS>(r0, bf0);
+    for (int j = 0; j < 4; ++j) {
+      const int row = wn + 16 * j + c;  // wswz(row) = wswz(c)
+      if constexpr (WBITS == 4) {
+        r.w[j][0] = lds_ld<uint32_t>(wb + row * 128 + ((pos << 4) ^ hc) + 4 * g);
+        r.s2[j] = lds_ld<uint32_t>(sb + row * 32);
+      } else {
+        const u2_t v =
+            lds_ld<u2_t>(wb + row * 128 + (((2 * pos + (g >> 1)) << 4) ^ hc) + 8 * (g & 1));
+        r.w[j][0] = v[0];
+        r.w[j][1] = v[1];
+        r.s2[j] = lds_ld<uint32_t>(sb + row * 16);
+      }
+    }
   }
-  auto kstep = [&](int i, h8_t (&bf)[4], h8_t (&bn)[4]) {
-    wait_copies<(S - 3) * R::kPerStage>();  // this wave's copies of step i+1 landed
-    ring_barrier();
-    ring_issue<WBITS>(ring + ((i + S - 1) % S) * R::kStage, X, W, SZ, M, N, K, m0, n0,
-                      kb0 + min(i + S - 1, nk - 1), wave, lane);
-    const uint8_t* st = ring + (i % S) * R::kStage;
-    h8_t af[8];
+
+  // Step i; the position in the super-step is a wave-uniform runtime value
+  // (an unrolled super-step keeps every position's LDS offsets in VGPRs).
+  // Entering: af = step i's X fragments, bf = step i's B (dequantised),
+  // rb1 = step i+1's raw B.  Leaving: af = step i+1's X, bf = step i+1's B,
+  // rb1 = step i+2's raw B (read two steps ahead, so that the dequantisation
+  // has its inputs in registers and can run between the MFMAs).
+  __device__ __forceinline__ void step(int i, f4_t (&acc)[16][4], h8_t (&af)[16], h8_t (&bf)[4],
+                                       BRaw<WBITS>& rb1) {
+    const int pos = i % KS;
+    if (pos == 1)  // this wave's copies of step i+1 landed
+      wait_copies<kAfter + R::kWCopies>();
+    else
+      wait_copies<kAfter>();
+    ring_barrier();  // everyone's; and every read of step i-1's stage is done
+    if (pos == 0) issue_w(i / KS + 1);
+    issue_x(i + kXStages - 1);
+    BRaw<WBITS> rb2;
+    load_b(i + 2, rb2);
+    __builtin_amdgcn_sched_barrier(0);
+    // 16 groups: 4 MFMAs of X fragment i8, its refill with the next step's
+    // fragment, and pair i8 % 4 of the next step's B fragment i8 / 4
+    u4_t bw[4];
+    h2_t nz, sc;
+    const lds8* xn = xst(i + 1) + xoff;
 #pragma unroll
-    for (int i8 = 0; i8 < 8; ++i8) af[i8] = *reinterpret_cast<const h8_t*>(st + xoff[i8]);
-    // step i+1's B fragments (raw reads now, dequantised between the MFMAs)
-    BRaw<WBITS> rn;
-    frag_load<WBITS>(ring + ((i + 1) % S) * R::kStage, rn, wn, c, g);
-#pragma unroll
-    for (int i8 = 0; i8 < 8; ++i8)
+    for (int i8 = 0; i8 < 16; ++i8) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[i8][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i8], bf[j], acc[i8][j], 0, 0, 0);
-    frag_dequant<WBITS>(rn, bn);
-    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
-#pragma unroll
-    for (int k = 0; k < 32; ++k) {
+      af[i8] = lds_ld<h8_t>(xn + 1024 * i8);
+      bw[i8 >> 2][i8 & 3] = dq_pair<WBITS>(rb1, i8 >> 2, i8 & 3, nz, sc);
+      // consumed here, so that the pair is computed inside its group
+      asm volatile("" ::"v"(bw[i8 >> 2][i8 & 3]));
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-  };
-  int i = 0;
-  for (; i + 1 < nk; i += 2) {
-    kstep(i, bf0, bf1);
-    kstep(i + 1, bf1, bf0);
+    h8_t bn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bn[j] = __builtin_bit_cast(h8_t, bw[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = bn[j];
+    rb1 = rb2;
   }
-  if (i < nk) kstep(i, bf0, bf1);
-  wait_copies<0>();  // no copy may land after the workgroup's LDS is released
-  // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block
+
+  __device__ void run(f4_t (&acc)[16][4]) {
+    // prologue: super-step 0's weights, then X steps 0 .. kXStages-2
+    issue_w(0);
 #pragma unroll
-  for (int i8 = 0; i8 < 8; ++i8)
+    for (int s = 0; s < kXStages - 1; ++s) issue_x(s);
+    wait_copies<R::kXCopies * (kXStages - 2)>();  // X step 0 (and the weights) landed
+    ring_barrier();
+    h8_t af[16], bf[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = n0 + wn + 16 * j + c;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm + 16 * i8 + 4 * g + r;
-        if (split)  // the whole 256 x 256 partial tile (the reduction skips the outside)
-          part[(((int64_t)sp * nst + slot) * RBM + (row - m0)) * RBN + (col - n0)] = acc[i8][j][r];
-        else if (row < M && col < N)
-          Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
-      }
+    for (int i8 = 0; i8 < 16; ++i8) af[i8] = lds_ld<h8_t>(xst(0) + xoff + 1024 * i8);
+    BRaw<WBITS> rb1;
+    {
+      BRaw<WBITS> r0;
+      load_b(0, r0);
+      frag_dequant<WBITS>(r0, bf);
     }
+    load_b(1, rb1);  // step 1 is in super-step 0 (KS >= 4)
+    for (int i = 0; i < nk; ++i) step(i, acc, af, bf, rb1);
+    wait_copies<0>();  // no copy may land after the ring is reused or released
+    ring_barrier();    // every wave's last fragment reads done before the next segment
+  }
+};
+
+template <int WBITS>
+__global__ __launch_bounds__(kRingThreads, 1) void gemm_ring_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, float* __restrict__ part, int M,
+    int N, int K, int dp, int sk, int U, int maxseg) {
+  using R = Ring<WBITS>;
+  __shared__ __align__(16) uint8_t ring[R::kBytes];
+  RingSeg<WBITS> sg;
+  // the ring's base as a value the compiler cannot see: it is LDS address 0,
+  // and with that known the per-stage offsets become per-lane registers
+  // instead of immediate offsets of the LDS reads
+  lds8* rb = (lds8*)ring;
+  asm volatile("" : "+s"(rb));
+  sg.ring = rb;
+  sg.X = X;
+  sg.W = W;
+  sg.SZ = SZ;
+  sg.M = M;
+  sg.N = N;
+  sg.K = K;
+  const int t = threadIdx.x;
+  sg.lane = t & 63;
+  sg.wave = t >> 6;
+  sg.wn = sg.wave * 64;
+  sg.c = sg.lane & 15;
+  sg.g = sg.lane >> 4;
+  sg.hc = wswz(sg.c) << 4;
+  // fragment i8 of a stage: rows 16 i8 + c, k labels 8g .. 8g+7 (piece g of
+  // the row, swizzled by (row >> 1) & 3 = (c >> 1) & 3) at xoff + 1024 i8
+  sg.xoff = sg.c * 64 + 16 * (sg.g ^ ((sg.c >> 1) & 3));
+  const int ntn = (N + RBN - 1) / RBN;
+  const int tiles = ntn * ((M + RBM - 1) / RBM);
+  const int nks = K / RBK;
+  const int b = blockIdx.x;
+  // unit range over the flattened (tile, unit) space of this block
+  int64_t lo, hi, TU = 0;
+  int w = 0;
+  if (b < dp) {
+    lo = (int64_t)b * U;
+    hi = lo + U;
+  } else {
+    // stream-K workgroup; consecutive workgroups (adjacent units, shared
+    // tiles and X rows) are placed on one XCD (blocks go to XCDs round-robin)
+    const int bb = b - dp;
+    w = (sk % 8 == 0) ? (b % 8) * (sk / 8) + bb / 8 : bb;
+    TU = (int64_t)(tiles - dp) * U;
+    lo = (int64_t)dp * U + sk_lo(w, TU, sk);
+    hi = (int64_t)dp * U + sk_lo(w + 1, TU, sk);
+  }
+  for (int64_t u = lo; u < hi;) {
+    const int tile = (int)(u / U);
+    const int64_t ue = min(hi, (int64_t)(tile + 1) * U);
+    const int ua = (int)(u - (int64_t)tile * U), ub = (int)(ue - (int64_t)tile * U);
+    sg.m0 = (tile / ntn) * RBM;
+    sg.n0 = (tile % ntn) * RBN;
+    sg.kb0 = ua * R::KS;
+    sg.nk = min(ub * R::KS, nks) - sg.kb0;
+    f4_t acc[16][4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+    sg.run(acc);
+    const bool whole = ua == 0 && ub == U;
+    float* pt = nullptr;
+    if (!whole) {
+      const int tl = tile - dp;
+      const int j = w - sk_owner((int64_t)tl * U, TU, sk);
+      pt = part + ((int64_t)tl * maxseg + j) * (RBM * RBN);
+    }
+    // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block.
+    // The lane index is re-read through an empty asm so that the compiler
+    // does not keep the store offsets live across the segment loop.
+    int tq = t;
+    asm volatile("" : "+v"(tq));
+    const int ec = tq & 15, eg = (tq >> 4) & 3, ewn = (tq >> 6) * 64;
+#pragma unroll
+    for (int i8 = 0; i8 < 16; ++i8)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cl = ewn + 16 * j + ec, col = sg.n0 + cl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rl = 16 * i8 + 4 * eg + r, row = sg.m0 + rl;
+          if (!whole)  // the whole 256 x 256 partial tile (the reduce skips the outside)
+            pt[rl * RBN + cl] = acc[i8][j][r];
+          else if (row < M && col < N)
+            Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
+        }
+      }
+    u = ue;
+  }
 }
 
-// Y = fp16(sum over s = 0 .. S-1 of part[s][slot]) for the nst split tiles
-// (tiles full .. full+nst-1), in split order (deterministic); one block per
-// (split tile, tile row), one thread per column.
+// Y = fp16(sum over the segments of each shared tile, in segment order);
+// one block per (stream-K tile, 4 tile rows), each thread 4 columns of one
+// row (16-byte loads), the loads of up to 8 segments in flight before they
+// are added in order.
+constexpr int kRedRows = 4;
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
                                                                  uint16_t* __restrict__ Y, int M,
-                                                                 int N, int full, int nst,
-                                                                 int S) {
-  const int slot = blockIdx.x / RBM, r = blockIdx.x % RBM, c = threadIdx.x;
-  const int tile = full + slot, ntn = (N + RBN - 1) / RBN;
-  const int row = (tile / ntn) * RBM + r, col = (tile % ntn) * RBN + c;
+                                                                 int N, int dp, int sk, int U,
+                                                                 int maxseg) {
+  constexpr int BPT = RBM / kRedRows;  // blocks per tile
+  const int tl = blockIdx.x / BPT;
+  const int r = (blockIdx.x % BPT) * kRedRows + (threadIdx.x >> 6);
+  const int c4 = (threadIdx.x & 63) * 4;
+  const int ntn = (N + RBN - 1) / RBN;
+  const int tiles = ntn * ((M + RBM - 1) / RBM);
+  const int64_t TU = (int64_t)(tiles - dp) * U;
+  const int w0 = sk_owner((int64_t)tl * U, TU, sk);
+  const int w1 = sk_owner((int64_t)tl * U + U - 1, TU, sk);
+  if (w1 == w0) return;  // written whole by one workgroup
+  const int tile = dp + tl;
+  const int row = (tile / ntn) * RBM + r, col = (tile % ntn) * RBN + c4;
   if (row >= M || col >= N) return;
-  const int64_t plane = (int64_t)nst * RBM * RBN;
-  const float* p = part + ((int64_t)slot * RBM + r) * RBN + c;
-  float v = p[0];
-  for (int z = 1; z < S; ++z) v += p[z * plane];
-  Y[(int64_t)row * N + col] = f2h(v);
+  const int nseg = w1 - w0 + 1;
+  const float* p = part + (int64_t)tl * maxseg * (RBM * RBN) + r * RBN + c4;
+  f4_t v = *reinterpret_cast<const f4_t*>(p);
+  for (int j0 = 1; j0 < nseg; j0 += 8) {
+    f4_t t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      t[q] = *reinterpret_cast<const f4_t*>(p + (int64_t)min(j0 + q, nseg - 1) * (RBM * RBN));
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (j0 + q < nseg) v += t[q];
+  }
+  uint16_t* y = Y + (int64_t)row * N + col;
+  if (col + 4 <= N && (N & 3) == 0) {
+    const uint32_t lo = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+    const uint32_t hi = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (col + q < N) y[q] = f2h(v[q]);
+  }
 }
 
 // ---------------------------------------------------------------------
@@ -852,78 +1091,79 @@ int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* 
   return skinny_run(x, w, sz, y, M, 2 * I, K, wbits, st, ws, ws_bytes, I);
 }
 
-bool gemm_ring_ok(int64_t M, int wbits) { return M >= RBM && wbits != 16; }
+// The ring kernel addresses X, W and the scale words with 32-bit byte offsets.
+bool gemm_ring_ok(int64_t M, int64_t N, int64_t K, int wbits) {
+  const int64_t lim = (int64_t)1 << 32;
+  return M >= RBM && wbits != 16 && M * K * 2 < lim && N * K * wbits / 8 < lim &&
+         N * (K / 32) * 4 < lim;
+}
 
-// Work split of the ring kernel: `full` tiles computed whole, the other
-// nst = tiles - full split S ways along K (kps steps each).
+// Work split of the ring kernel (see gemm_ring_kernel): dp whole tiles,
+// then sk stream-K workgroups over the other tiles.
 struct RingPlan {
-  int full = 0, S = 1, kps = 0, nst = 0;
-  size_t ws = 0;  // fp32 partials: S * nst * 256 * 256 * 4 bytes
+  int dp = 0, sk = 0, U = 1, maxseg = 1;
+  size_t ws = 0;  // fp32 partials: (tiles - dp) * maxseg * 256 * 256 * 4 bytes
 };
 
-RingPlan ring_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
-  // Estimated time: rounds of one workgroup per CU (256), a whole tile's K
-  // loop at ~3.7 TFLOP/s per CU (measured), split tiles taking 1/S of it,
-  // plus the partials written and read back at ~5 TB/s.  Candidates: no
-  // split; every tile split S ways (few tiles); only the tiles of a last,
-  // partial round split S ways (full = the tiles of the complete rounds).
+constexpr int kRingCUs = 256;  // MI355X compute units: one ring workgroup each (LDS-bound)
+
+// Host restatement of sk_lo / sk_owner (the kernel's unit split).
+static int64_t host_sk_lo(int64_t w, int64_t TU, int64_t sk) { return w * TU / sk; }
+static int64_t host_sk_owner(int64_t u, int64_t TU, int64_t sk) {
+  int64_t w = u * sk / TU;
+  while (w + 1 < sk && host_sk_lo(w + 1, TU, sk) <= u) ++w;
+  while (w > 0 && host_sk_lo(w, TU, sk) > u) --w;
+  return w;
+}
+
+RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  // Every CU gets the same number of K units: when the tiles do not fill
+  // whole rounds of 256 workgroups, the last one to two rounds' tiles are
+  // shared out by stream-K (at least a whole tile's work per workgroup when
+  // there are more tiles than CUs, so that a tile is cut at most twice).
   const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
-  const int64_t nk = K / RBK;
-  const double tile_us = 2.0 * RBM * RBN * (double)K / 3.7e6;
-  const double part_us = (double)RBM * RBN * 8 / 5e6;  // one partial tile, out and back
-  RingPlan best;
-  best.full = (int)tiles;
-  best.kps = (int)nk;
-  double best_us = (double)((tiles + 255) / 256) * tile_us;
-  auto consider = [&](int64_t full, int S) {
-    const int64_t nst = tiles - full;
-    if (S < 2 || nst <= 0 || nk / S < 8) return;
-    const size_t ws = (size_t)S * nst * RBM * RBN * 4;
-    if (ws > ws_bytes) return;
-    const int64_t rounds_full = (full + 255) / 256, rounds_split = (nst * S + 255) / 256;
-    const double us = rounds_full * tile_us + rounds_split * tile_us / S + S * nst * part_us;
-    if (us < best_us) {
-      best_us = us;
-      best.full = (int)full;
-      best.S = S;
-      best.nst = (int)nst;
-      best.ws = ws;
-    }
-  };
-  for (int S = 2; S <= kMaxGemmSplits; ++S) {
-    consider(0, S);
-    if (tiles > 256 && tiles % 256) consider(tiles - tiles % 256, S);
-  }
-  if (const int v = tuning().gemm_splits.load()) {  // measurement override: every tile split
-    const size_t ws = (size_t)v * tiles * RBM * RBN * 4;
-    if (v >= 2 && v <= kMaxGemmSplits && nk / v >= 1 && ws <= ws_bytes) {
-      best.full = 0;
-      best.S = v;
-      best.nst = (int)tiles;
-      best.ws = ws;
-    } else if (v == 1) {
-      best = RingPlan();
-      best.full = (int)tiles;
-    }
-  }
-  best.kps = best.S > 1 ? (int)((nk + best.S - 1) / best.S) : (int)nk;
-  if (best.S > 1) best.S = (int)((nk + best.kps - 1) / best.kps);  // every split non-empty
-  if (best.S == 1) {
-    best.full = (int)tiles;
-    best.nst = 0;
-    best.ws = 0;
+  const int KS = wbits == 4 ? Ring<4>::KS : Ring<8>::KS;
+  RingPlan pl;
+  pl.U = (int)((K / RBK + KS - 1) / KS);
+  int64_t dp = tiles, sk = 0;
+  const int v = tuning().gemm_splits.load();  // measurement override
+  if (v >= 2) {                                // about v segments per tile, all tiles shared
+    dp = 0;
+    sk = std::min<int64_t>(tiles * v, tiles * pl.U);
+  } else if (v == 1 || tiles % kRingCUs == 0) {
+    dp = tiles;
+  } else if (tiles > kRingCUs) {
+    dp = (tiles / kRingCUs - 1) * kRingCUs;
+    sk = kRingCUs;
   } else {
-    best.ws = (size_t)best.S * best.nst * RBM * RBN * 4;
+    dp = 0;
+    sk = std::min<int64_t>(kRingCUs, tiles * pl.U);
   }
-  return best;
+  if (sk > 0) {
+    const int64_t TU = (tiles - dp) * pl.U;
+    int64_t maxseg = 1;
+    for (int64_t t = 0; t < tiles - dp; ++t)
+      maxseg = std::max(maxseg, host_sk_owner(t * pl.U + pl.U - 1, TU, sk) -
+                                    host_sk_owner(t * pl.U, TU, sk) + 1);
+    const size_t ws = maxseg > 1 ? (size_t)(tiles - dp) * maxseg * RBM * RBN * 4 : 0;
+    if (ws <= ws_bytes) {
+      pl.dp = (int)dp;
+      pl.sk = (int)sk;
+      pl.maxseg = (int)maxseg;
+      pl.ws = ws;
+      return pl;
+    }
+  }
+  pl.dp = (int)tiles;  // whole tiles only
+  return pl;
 }
 
 int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
-  return gemm_ring_ok(M, wbits) ? ring_plan(M, N, K, ws_bytes).S : 1;
+  return gemm_ring_ok(M, N, K, wbits) ? ring_plan(M, N, K, wbits, ws_bytes).maxseg : 1;
 }
 
 size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
-  return gemm_ring_ok(M, wbits) ? ring_plan(M, N, K, (size_t)-1).ws : 0;
+  return gemm_ring_ok(M, N, K, wbits) ? ring_plan(M, N, K, wbits, (size_t)-1).ws : 0;
 }
 
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
@@ -932,20 +1172,22 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
-  if (gemm_ring_ok(M, wbits)) {
-    const RingPlan pl = ring_plan(M, N, K, ws ? ws_bytes : 0);
-    float* part = pl.S > 1 ? static_cast<float*>(ws) : nullptr;
-    const unsigned blocks = (unsigned)(pl.full + (int64_t)pl.nst * pl.S);
+  if (gemm_ring_ok(M, N, K, wbits)) {
+    const RingPlan pl = ring_plan(M, N, K, wbits, ws ? ws_bytes : 0);
+    float* part = pl.ws ? static_cast<float*>(ws) : nullptr;
+    const unsigned blocks = (unsigned)(pl.dp + pl.sk);
     if (wbits == 4)
       hipLaunchKernelGGL(gemm_ring_kernel<4>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
-                         yp, part, (int)M, (int)N, (int)K, pl.full, pl.S, pl.kps);
+                         yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U, pl.maxseg);
     else
       hipLaunchKernelGGL(gemm_ring_kernel<8>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
-                         yp, part, (int)M, (int)N, (int)K, pl.full, pl.S, pl.kps);
+                         yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U, pl.maxseg);
     R4Q_TRY(launch_status("gemm_ring"));
-    if (pl.S > 1) {
-      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)(pl.nst * RBM)), dim3(256), 0,
-                         st, part, yp, (int)M, (int)N, pl.full, pl.nst, pl.S);
+    if (pl.ws) {
+      const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
+      const unsigned rb = (unsigned)((tiles - pl.dp) * (RBM / kRedRows));
+      hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(rb), dim3(256), 0, st, part, yp, (int)M,
+                         (int)N, pl.dp, pl.sk, pl.U, pl.maxseg);
       R4Q_TRY(launch_status("gemm_splitk_reduce"));
     }
     return R4Q_OK;
