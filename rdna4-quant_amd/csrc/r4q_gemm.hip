@@ -594,11 +594,18 @@ struct RingSeg {
     rb1 = rb2;
   }
 
-  __device__ void run(f4_t (&acc)[16][4]) {
-    // prologue: super-step 0's weights, then X steps 0 .. kXStages-2
+  // the segment's first copies: super-step 0's weights, X steps 0 .. kXStages-2
+  __device__ __forceinline__ void start() {
     issue_w(0);
 #pragma unroll
     for (int s = 0; s < kXStages - 1; ++s) issue_x(s);
+  }
+
+  // the segment's K loop, after start(); nothing else may have been issued
+  // to global memory since start() but stores (they retire before the count
+  // below is reached only if they were issued earlier, which costs time, not
+  // correctness)
+  __device__ void run(f4_t (&acc)[16][4]) {
     wait_copies<R::kXCopies * (kXStages - 2)>();  // X step 0 (and the weights) landed
     ring_barrier();
     h8_t af[16], bf[4];
@@ -666,64 +673,86 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemm_ring_kernel(
     lo = (int64_t)dp * U + sk_lo(w, TU, sk);
     hi = (int64_t)dp * U + sk_lo(w + 1, TU, sk);
   }
-  for (int64_t u = lo; u < hi;) {
-    const int tile = (int)(u / U);
-    const int64_t ue = min(hi, (int64_t)(tile + 1) * U);
-    const int ua = (int)(u - (int64_t)tile * U), ub = (int)(ue - (int64_t)tile * U);
+  // segment starting at unit u: sets the ring's tile and K range
+  auto set_seg = [&](int64_t u, int64_t& ue, int& ua, int& ub, int& tile) {
+    tile = (int)(u / U);
+    ue = min(hi, (int64_t)(tile + 1) * U);
+    ua = (int)(u - (int64_t)tile * U);
+    ub = (int)(ue - (int64_t)tile * U);
     sg.m0 = (tile / ntn) * RBM;
     sg.n0 = (tile % ntn) * RBN;
     sg.kb0 = ua * R::KS;
     sg.nk = min(ub * R::KS, nks) - sg.kb0;
+  };
+  int64_t u = lo, ue = lo;
+  int ua = 0, ub = 0, tile = 0;
+  if (u < hi) {
+    set_seg(u, ue, ua, ub, tile);
+    sg.start();
+  }
+  while (u < hi) {
     f4_t acc[16][4];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
     sg.run(acc);
+    const int ctile = tile, cm0 = sg.m0, cn0 = sg.n0;
     const bool whole = ua == 0 && ub == U;
-    float* pt = nullptr;
-    if (!whole) {
-      const int tl = tile - dp;
-      const int j = w - sk_owner((int64_t)tl * U, TU, sk);
-      pt = part + ((int64_t)tl * maxseg + j) * (RBM * RBN);
+    // the next segment's first copies go out before this one's results
+    u = ue;
+    if (u < hi) {
+      set_seg(u, ue, ua, ub, tile);
+      sg.start();
     }
-    // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block.
     // The lane index is re-read through an empty asm so that the compiler
     // does not keep the store offsets live across the segment loop.
     int tq = t;
     asm volatile("" : "+v"(tq));
-    const int ec = tq & 15, eg = (tq >> 4) & 3, ewn = (tq >> 6) * 64;
+    if (!whole) {
+      // fp32 partial in the accumulator layout: float4 of (wave, i8, j, lane)
+      // at ((wave * 16 + i8) * 4 + j) * 64 + lane (16-byte stores, 1 KB per
+      // wave instruction); gemm_splitk_reduce_kernel reads the same layout
+      const int tl = ctile - dp;
+      const int j = w - sk_owner((int64_t)tl * U, TU, sk);
+      f4_t* pt = reinterpret_cast<f4_t*>(part + ((int64_t)tl * maxseg + j) * (RBM * RBN));
+      pt += (tq >> 6) * (16 * 4 * 64) + (tq & 63);
 #pragma unroll
-    for (int i8 = 0; i8 < 16; ++i8)
+      for (int i8 = 0; i8 < 16; ++i8)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int cl = ewn + 16 * j + ec, col = sg.n0 + cl;
+        for (int jj = 0; jj < 4; ++jj) pt[(i8 * 4 + jj) * 64] = acc[i8][jj];
+    } else {
+      // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block
+      const int ec = tq & 15, eg = (tq >> 4) & 3, ewn = (tq >> 6) * 64;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int rl = 16 * i8 + 4 * eg + r, row = sg.m0 + rl;
-          if (!whole)  // the whole 256 x 256 partial tile (the reduce skips the outside)
-            pt[rl * RBN + cl] = acc[i8][j][r];
-          else if (row < M && col < N)
-            Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
+      for (int i8 = 0; i8 < 16; ++i8)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int col = cn0 + ewn + 16 * jj + ec;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = cm0 + 16 * i8 + 4 * eg + r;
+            if (row < M && col < N) Y[(int64_t)row * N + col] = f2h(acc[i8][jj][r]);
+          }
         }
-      }
-    u = ue;
+    }
   }
 }
 
-// Y = fp16(sum over the segments of each shared tile, in segment order);
-// one block per (stream-K tile, 4 tile rows), each thread 4 columns of one
-// row (16-byte loads), the loads of up to 8 segments in flight before they
-// are added in order.
-constexpr int kRedRows = 4;
+// Y = fp16(sum over the segments of each shared tile, in segment order).
+// Partials are in the accumulator layout of gemm_ring_kernel (float4 of
+// (wave, i8, j, lane)); a thread takes lanes 16g + 4q .. + 3 of one
+// (wave, i8, j) -- 64 contiguous bytes, rows 16 i8 + 4g .. + 3 x columns
+// 64 wave + 16 j + 4q .. + 3 of the tile -- and writes 4 x 4 outputs.  The
+// loads of up to 8 segments are in flight before they are added in order.
+constexpr int kRedThreadsPerTile = RBM * RBN / 16;
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
                                                                  uint16_t* __restrict__ Y, int M,
                                                                  int N, int dp, int sk, int U,
                                                                  int maxseg) {
-  constexpr int BPT = RBM / kRedRows;  // blocks per tile
-  const int tl = blockIdx.x / BPT;
-  const int r = (blockIdx.x % BPT) * kRedRows + (threadIdx.x >> 6);
-  const int c4 = (threadIdx.x & 63) * 4;
+  const int gt = blockIdx.x * 256 + threadIdx.x;
+  const int tl = gt / kRedThreadsPerTile, x = gt % kRedThreadsPerTile;
+  const int q = x & 3, g = (x >> 2) & 3, j = (x >> 4) & 3, i8 = (x >> 6) & 15, wv = x >> 10;
   const int ntn = (N + RBN - 1) / RBN;
   const int tiles = ntn * ((M + RBM - 1) / RBM);
   const int64_t TU = (int64_t)(tiles - dp) * U;
@@ -731,29 +760,43 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   const int w1 = sk_owner((int64_t)tl * U + U - 1, TU, sk);
   if (w1 == w0) return;  // written whole by one workgroup
   const int tile = dp + tl;
-  const int row = (tile / ntn) * RBM + r, col = (tile % ntn) * RBN + c4;
-  if (row >= M || col >= N) return;
+  const int row0 = (tile / ntn) * RBM + 16 * i8 + 4 * g;
+  const int col0 = (tile % ntn) * RBN + 64 * wv + 16 * j + 4 * q;
+  if (row0 >= M || col0 >= N) return;
   const int nseg = w1 - w0 + 1;
-  const float* p = part + (int64_t)tl * maxseg * (RBM * RBN) + r * RBN + c4;
-  f4_t v = *reinterpret_cast<const f4_t*>(p);
-  for (int j0 = 1; j0 < nseg; j0 += 8) {
-    f4_t t[8];
+  const f4_t* p = reinterpret_cast<const f4_t*>(part + (int64_t)tl * maxseg * (RBM * RBN)) +
+                  ((wv * 16 + i8) * 4 + j) * 64 + 16 * g + 4 * q;
+  constexpr int64_t kSeg = RBM * RBN / 4;  // float4 per segment
+  f4_t v[4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      t[q] = *reinterpret_cast<const f4_t*>(p + (int64_t)min(j0 + q, nseg - 1) * (RBM * RBN));
+  for (int l = 0; l < 4; ++l) v[l] = p[l];
+  for (int j0 = 1; j0 < nseg; j0 += 4) {
+    f4_t t[4][4];
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (j0 + q < nseg) v += t[q];
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) t[s][l] = p[(int64_t)min(j0 + s, nseg - 1) * kSeg + l];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      if (j0 + s < nseg)
+#pragma unroll
+        for (int l = 0; l < 4; ++l) v[l] += t[s][l];
   }
-  uint16_t* y = Y + (int64_t)row * N + col;
-  if (col + 4 <= N && (N & 3) == 0) {
-    const uint32_t lo = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
-    const uint32_t hi = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
-    *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
-  } else {
+  // v[l][r]: row row0 + r, column col0 + l
+  const bool vec = col0 + 4 <= N && (N & 3) == 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (col + q < N) y[q] = f2h(v[q]);
+  for (int r = 0; r < 4; ++r) {
+    if (row0 + r >= M) break;
+    uint16_t* y = Y + (int64_t)(row0 + r) * N + col0;
+    if (vec) {
+      const uint32_t lo = (uint32_t)f2h(v[0][r]) | ((uint32_t)f2h(v[1][r]) << 16);
+      const uint32_t hi = (uint32_t)f2h(v[2][r]) | ((uint32_t)f2h(v[3][r]) << 16);
+      *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
+    } else {
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        if (col0 + l < N) y[l] = f2h(v[l][r]);
+    }
   }
 }
 
@@ -1185,7 +1228,7 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
     R4Q_TRY(launch_status("gemm_ring"));
     if (pl.ws) {
       const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
-      const unsigned rb = (unsigned)((tiles - pl.dp) * (RBM / kRedRows));
+      const unsigned rb = (unsigned)((tiles - pl.dp) * (kRedThreadsPerTile / 256));
       hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(rb), dim3(256), 0, st, part, yp, (int)M,
                          (int)N, pl.dp, pl.sk, pl.U, pl.maxseg);
       R4Q_TRY(launch_status("gemm_splitk_reduce"));
