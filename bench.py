@@ -166,15 +166,39 @@ def prefill_gemm_leg(dev, iters=20):
     """Config 3: Y[512, N] = X[512, K] deq(W)^T with INT4 weights (config 0's
     distribution), (K, N) = (5120, 17408) and (17408, 5120), through
     r4q_gemm_ws with the split-K workspace the library asks for.  HIP events
-    on a private stream; returns {shape: {us, tflops, frac, splits}}."""
+    on a private stream; returns {shape: {us, tflops, frac, workspace_mb,
+    reference_strategy}}.
+
+    `reference_strategy` times the reference's own prefill projection on the
+    same box (dequant_matmul_out, hip:1973-1988: the whole fp16 weight
+    materialised by a dequantisation kernel, then the vendor GEMM through
+    at::mm_out): r4q_dequant_int4 (bit-identical to the reference's
+    dequant_int4_kernel) into an fp16 [N, K] buffer, then torch's
+    F.linear(x, w) (rocBLAS / hipBLASLt, the library at::mm_out calls)."""
     import ctypes as C
 
     import torch
+    import torch.nn.functional as F
 
     import r4q_lib as R
     import r4q_synth as S
     res = {}
     st = torch.cuda.Stream(dev)
+
+    def timed(fn, n):
+        with torch.cuda.stream(st):
+            for _ in range(5):
+                fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(st):
+            e0.record(st)
+            for _ in range(n):
+                fn()
+            e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / n
+
     for K, N in ((5120, 17408), (17408, 5120)):
         M = 512
         g = S.gen(3)
@@ -190,21 +214,24 @@ def prefill_gemm_leg(dev, iters=20):
             R.call("r4q_gemm_ws", X.data_ptr(), Wd.data_ptr(), SZ.data_ptr(), Y.data_ptr(), M, N,
                    K, 4, ws.data_ptr(), nws.value, st.cuda_stream)
 
-        for _ in range(5):
-            launch()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        for _ in range(iters):
-            launch()
-        e1.record(st)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / iters
+        us = timed(launch, iters)
         tflops = 2.0 * M * N * K / us / 1e6
+        # the reference's strategy: fp16 weight materialised, then the vendor GEMM
+        W16 = torch.empty(N, K, dtype=torch.float16, device=dev)
+
+        def deq():
+            R.call("r4q_dequant_int4", Wd.data_ptr(), SZ.data_ptr(), W16.data_ptr(), N, K,
+                   st.cuda_stream)
+
+        deq_us = timed(deq, iters)
+        mm_us = timed(lambda: F.linear(X, W16), iters)
         res[f"{K}x{N}"] = {"us": round(us, 2), "tflops": round(tflops, 1),
                            "frac": round(tflops / MFMA_FP16_PEAK_TFLOPS, 4),
-                           "splits": nws.value // (M * N * 4) if nws.value else 1}
-        del X, Wd, SZ, Y, ws
+                           "workspace_mb": round(nws.value / 2**20, 1),
+                           "reference_strategy": {"dequant_us": round(deq_us, 2),
+                                                  "vendor_gemm_us": round(mm_us, 2),
+                                                  "us": round(deq_us + mm_us, 2)}}
+        del X, Wd, SZ, Y, ws, W16
     return res
 
 
@@ -515,8 +542,11 @@ def main():
     torch.cuda.empty_cache()
     pgemm = {} if args.decode_only else prefill_gemm_leg(dev)
     for k, v in pgemm.items():
+        rs = v["reference_strategy"]
         log(f"prefill GEMM 512x{k.replace('x', ' -> ')} INT4: {v['us']:.1f} us, "
-            f"{v['tflops']:.0f} TFLOP/s ({v['frac'] * 100:.1f}% of fp16 MFMA peak)")
+            f"{v['tflops']:.0f} TFLOP/s ({v['frac'] * 100:.1f}% of fp16 MFMA peak); "
+            f"reference strategy (dequantise + vendor fp16 GEMM): {rs['dequant_us']:.1f} + "
+            f"{rs['vendor_gemm_us']:.1f} = {rs['us']:.1f} us")
     torch.cuda.empty_cache()
 
     log("building synthetic model")

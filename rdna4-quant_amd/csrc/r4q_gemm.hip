@@ -220,15 +220,13 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 }
 
 // ---------------------------------------------------------------------
-// Prefill GEMM for M >= 256 with INT4 / INT8 weights: a workgroup of 8 waves
-// (2 per SIMD) owns a 256 x 256 output tile, each wave a 128 x 64 sub-tile
-// (8 x 4 MFMA tiles, 128 fp32 accumulators per lane).
+// Prefill GEMM for M >= 256 with INT4 / INT8 weights: a workgroup of 4 waves
+// (one per SIMD) owns a 256 x 256 output tile, each wave 256 rows x 64
+// columns (16 x 4 MFMA tiles, 256 fp32 accumulators per lane, in AGPRs).
 // The K loop of the 128 x 128 kernel above is bound by global-load latency
-// (one 32-wide K step in flight, ~1.3 us per step on MI355X).  Here X and
-// the raw weight bytes (plus the (scale, zero) words) of a K step land in
-// LDS by direct global->LDS copies (global_load_lds_dwordx4 / _dword) in a
-// ring of Ring::kStages stages, so that several steps are in flight while
-// one is multiplied, without holding them in VGPRs.
+// (one 32-wide K step in flight, ~1.3 us per step on MI355X); here the
+// operands arrive through LDS rings filled by direct global->LDS copies, so
+// that several steps are in flight without holding them in VGPRs.
 // X of a K step (16 KB) lands in LDS by direct global->LDS copies
 // (global_load_lds_dwordx4) in a ring of kXStages stages; the raw weights
 // and their (scale, zero) words arrive per super-step of Ring::KS K steps
