@@ -211,3 +211,59 @@ def test_gemm_silu_fwht_rejects_unsplit_shapes(dev):
         with pytest.raises(RuntimeError):
             R.call("r4q_gemm_silu_fwht_ws", x.data_ptr(), wd.data_ptr(), sd.data_ptr(),
                    y.data_ptr(), M, II, K, 4, ws.data_ptr(), nbytes, st)
+
+
+def _ref32(x, w, sz, bits):
+    """x @ deq(W)^T in float32 on the CPU: the oracle's dequantisation (bit-exact
+    to the kernels') and a library matmul, for shapes too large for the
+    float64 oracle GEMM to finish in seconds."""
+    W = torch.from_numpy(O.dequant(w.numpy(), sz.numpy(), bits)).float()
+    return (x.float() @ W.T).numpy()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_ring_gemm_whole_tile_rounds_then_stream_k(dev, bits):
+    """576 tiles of 256 x 256 (more than two rounds of 256 workgroups): the
+    first round's tiles are computed whole, the remaining 320 tiles' K units
+    are shared by 256 stream-K workgroups (tails and heads of tiles as fp32
+    partials, summed in segment order)."""
+    import ctypes as C
+    import r4q_lib as R
+    M, N, K = 2304, 16384, 768
+    g = S.gen(91 + bits)
+    w, sz = S.weight(N, K, bits, g)
+    x = (torch.randn(M, K, generator=g) * 0.5).half()
+    nws = C.c_size_t(0)
+    R.call("r4q_gemm_workspace_bytes", M, N, K, bits, C.byref(nws))
+    assert nws.value > 0
+    got = int4_hip.dbg_gemm(x.to(dev), w.to(dev), sz.to(dev), M, N, K).float().cpu().numpy()
+    want = _ref32(x, w, sz, bits)
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, want) <= TOL
+    for r in (0, 255, 256, 1023, 1024, M - 1):  # rows of the whole-tile and shared rounds
+        assert rel_l2(got[r], want[r]) <= TOL, r
+
+
+@pytest.mark.parametrize("splits", [2, 5])
+def test_ring_gemm_forced_split_counts(dev, splits):
+    """The gemm_splits override shares every tile among about `splits`
+    workgroups; results equal the default plan's within fp32 rounding and
+    the oracle's within the GEMM tolerance."""
+    import ctypes as C
+    import r4q_lib as R
+    M, N, K = 512, 1280, 4096
+    g = S.gen(17 + splits)
+    w, sz = S.int4_weight(N, K, g)
+    x = torch.randn(M, K, generator=g).half()
+    X, Wd, SZ = x.to(dev), w.to(dev), sz.to(dev)
+    base = int4_hip.dbg_gemm(X, Wd, SZ, M, N, K).float().cpu().numpy()
+    try:
+        R.tune("gemm_splits", splits)
+        nws = C.c_size_t(0)
+        R.call("r4q_gemm_workspace_bytes", M, N, K, 4, C.byref(nws))
+        assert nws.value > 0
+        got = int4_hip.dbg_gemm(X, Wd, SZ, M, N, K).float().cpu().numpy()
+    finally:
+        R.tune("gemm_splits", 0)
+    assert rel_l2(got, base) <= 1e-3
+    assert rel_l2(got, O.gemm(x.numpy(), w.numpy(), sz.numpy(), 4)) <= TOL
