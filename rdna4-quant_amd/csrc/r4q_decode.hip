@@ -92,7 +92,7 @@ struct Bufs {
   float* amax;  // argmax partials
 };
 
-constexpr int kArgmaxBlocks = 64;
+constexpr int kArgmaxBlocks = 64;  // <= 64: stage 2 reduces them in one wave
 
 int validate(const r4q_model* m, int64_t B, Dims& dm) {
   R4Q_REQUIRE(m && m->layers, "decode: null model");
@@ -318,6 +318,20 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+// (value, index) pair reduction across a wave with `better` (the larger
+// value, then the lower index); every lane ends with the wave's best.
+__device__ __forceinline__ void wave_best(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o);
+    const int oi = __shfl_xor(i, o);
+    if (better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
 // Stage 1: per (block, row) max and first index of the max.
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const uint16_t* __restrict__ logits,
                                                              int64_t V, float* __restrict__ part) {
@@ -333,52 +347,58 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const uint16_t* __r
       bi = (int)i;
     }
   }
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s && better(sv[threadIdx.x + s], si[threadIdx.x + s], sv[threadIdx.x],
-                                  si[threadIdx.x])) {
-      sv[threadIdx.x] = sv[threadIdx.x + s];
-      si[threadIdx.x] = si[threadIdx.x + s];
-    }
-    __syncthreads();
+  wave_best(bv, bi);
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    part[(b * gridDim.x + blockIdx.x) * 2] = sv[0];
-    part[(b * gridDim.x + blockIdx.x) * 2 + 1] = __int_as_float(si[0]);
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    part[(b * gridDim.x + blockIdx.x) * 2] = bv;
+    part[(b * gridDim.x + blockIdx.x) * 2 + 1] = __int_as_float(bi);
   }
 }
 
-// Stage 2 (one block per row): final argmax, token id out, embedding gather
-// into the next step's hidden state.
+// Stage 2 (one block per row): final argmax over the nblk (<= 64) partials
+// by one wave, token id out, embedding gather into the next step's hidden
+// state; with `advance` (one row only) also the position / step counters
+// that advance_kernel moves otherwise.
 __global__ __launch_bounds__(256) void argmax_embed_kernel(
     const float* __restrict__ part, int nblk, const uint16_t* __restrict__ embed, int64_t vocab,
     int D, uint16_t* __restrict__ h, int64_t* __restrict__ ids, int64_t* __restrict__ tokens_out,
-    const int* __restrict__ state, int step_host, int B) {
+    int* __restrict__ state, int step_host, int B, int advance) {
   const int b = blockIdx.x;
   __shared__ int tok;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64) {
+    const int k = threadIdx.x;
     float bv = -INFINITY;
-    int bi = 0;
-    bool any = false;
-    for (int k = 0; k < nblk; ++k) {
-      const float v = part[(b * nblk + k) * 2];
-      const int i = __float_as_int(part[(b * nblk + k) * 2 + 1]);
-      if (i == 0x7FFFFFFF) continue;
-      if (!any || better(v, i, bv, bi)) {
-        bv = v;
-        bi = i;
-        any = true;
+    int bi = 0x7FFFFFFF;  // blocks past nblk and empty blocks lose every comparison
+    if (k < nblk) {
+      bv = part[(b * nblk + k) * 2];
+      bi = __float_as_int(part[(b * nblk + k) * 2 + 1]);
+    }
+    wave_best(bv, bi);
+    if (threadIdx.x == 0) {
+      if (bi >= vocab) bi = 0;
+      tok = bi;
+      ids[b] = bi;
+      const int step = state ? state[kStep] : step_host;
+      if (tokens_out) tokens_out[(int64_t)step * B + b] = bi;
+      if (advance) {
+        state[kPos] += 1;
+        state[kSeq] = state[kPos] + 1;
+        state[kStep] += 1;
       }
     }
-    if (bi >= vocab) bi = 0;
-    tok = bi;
-    ids[b] = bi;
-    const int step = state ? state[kStep] : step_host;
-    if (tokens_out) tokens_out[(int64_t)step * B + b] = bi;
   }
   __syncthreads();
   const u4_t* src = reinterpret_cast<const u4_t*>(embed + (int64_t)tok * D);
@@ -420,11 +440,15 @@ int enqueue_sample(const r4q_model* m, const Dims& dm, int64_t B, const Bufs& bf
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxBlocks, (unsigned)B), dim3(256), 0, st,
                      bf.logits, m->lm_N, bf.amax);
   R4Q_TRY(launch_status("argmax"));
+  // one row: the gather kernel also advances the counters (a single block
+  // reads the step before it moves it); several rows: a kernel of its own
+  const int fold = device_step && B == 1;
   hipLaunchKernelGGL(argmax_embed_kernel, dim3((unsigned)B), dim3(256), 0, st, bf.amax,
                      kArgmaxBlocks, static_cast<const uint16_t*>(m->embed), m->vocab, dm.D, bf.h,
-                     bf.ids, tokens_out, device_step ? bf.state : nullptr, step_host, (int)B);
+                     bf.ids, tokens_out, device_step ? bf.state : nullptr, step_host, (int)B,
+                     fold);
   R4Q_TRY(launch_status("argmax_embed"));
-  if (device_step) {
+  if (device_step && !fold) {
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, st, bf.state);
     R4Q_TRY(launch_status("advance"));
   }
