@@ -110,10 +110,13 @@ R4Q_API int r4q_gemv(const void* x, const void* w, const void* sz, void* y,
 R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
              int64_t M, int64_t N, int64_t K, int wbits, void* stream);
 /* Device workspace (bytes, written to *bytes; 0: none) that lets r4q_gemm_ws
- * split the K loop of an M >= 256 INT4/INT8 product over more workgroups
- * (fp32 partials, summed in a fixed order: the result does not depend on
- * the split).  Same role as the rocBLAS workspace behind the reference's
- * at::mm_out in dequant_matmul_out (hip:1973-1988). */
+ * split K loops over more workgroups: for M >= 256 INT4/INT8 the K units of
+ * the output tiles are shared evenly by the CUs (stream-K), for 2 <= M <= 16
+ * the weight tiles split along K.  Split tiles keep fp32 partials in the
+ * workspace, summed in a fixed order (deterministic for a given shape and
+ * workspace size; within fp32 rounding of the unsplit product).  Same role
+ * as the rocBLAS workspace behind the reference's at::mm_out in
+ * dequant_matmul_out (hip:1973-1988). */
 R4Q_API int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbits,
                                      size_t* bytes);
 /* r4q_gemm with a caller-owned workspace of ws_bytes (NULL / 0: no split). */
@@ -370,8 +373,8 @@ R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hid
  * choice).  Knobs: "gemv_lpr" (lanes per GEMV row: 16..256, power of two),
  * "gemv_wgs" (GEMV workgroup cap, 1..65536), "gemv_ub" (GEMV steps in flight
  * per lane, 1..2), "attn_splits" (flash-decode splits, 1..128), "skinny_splits"
- * (skinny GEMM K splits, 1..8), "gemm_splits" (ring GEMM K splits of every
- * tile, 1..16).  Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS,
+ * (skinny GEMM K splits, 1..8), "gemm_splits" (ring GEMM: 1 = whole tiles
+ * only, 2..16 = stream-K with about that many workgroups per tile).  Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS,
  * R4Q_GEMV_UB, R4Q_ATTN_SPLITS, R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, read once.
  * Results do not depend on these choices beyond fp32 summation order
  * (split counts) -- they exist for sweeps and tests. */

@@ -29,7 +29,7 @@ int launch_status(const char* what);
 //   gemv_ub       R4Q_GEMV_UB       GEMV steps in flight per lane: 1 or 2
 //   attn_splits   R4Q_ATTN_SPLITS   flash-decode splits: 1 .. 128
 //   skinny_splits R4Q_SKINNY_SPLITS skinny-GEMM K splits: 1 .. 8
-//   gemm_splits   R4Q_GEMM_SPLITS   ring-GEMM K splits of every tile: 1 .. 16
+//   gemm_splits   R4Q_GEMM_SPLITS   ring GEMM: 1 whole tiles, 2 .. 16 stream-K workgroups per tile
 struct Tuning {
   std::atomic<int> gemv_lpr{0}, gemv_wgs{0}, gemv_ub{0};
   std::atomic<int> attn_splits{0}, skinny_splits{0}, gemm_splits{0};
