@@ -270,18 +270,23 @@ constexpr int kXStages = 4;                   // X ring depth (one K step per st
 
 template <int WBITS>
 struct Ring {
+  static constexpr bool kF16 = WBITS == 16;
   // K steps per weight super-step: 128 bytes of every weight row, fetched
-  // as whole cache lines (INT4: 8 steps of 16 bytes, INT8: 4 of 32)
-  static constexpr int KS = WBITS == 4 ? 8 : 4;
-  static constexpr int kX = RBM * RBK * 2;    // one X stage: 16 KB
-  static constexpr int kW = RBN * 128;        // one super-step of raw weights: 32 KB
-  static constexpr int kS = RBN * KS * 4;     // its (scale, zero) words: 8 KB / 4 KB
+  // as whole cache lines (INT4: 8 steps of 16 bytes, INT8: 4 of 32).  FP16
+  // weights (64 bytes per row and step) travel with X instead: each X stage
+  // holds the step's X (16 KB) and its weights (16 KB).
+  static constexpr int KS = WBITS == 4 ? 8 : WBITS == 8 ? 4 : 1;
+  static constexpr int kXPart = RBM * RBK * 2;          // X of a step: 16 KB
+  static constexpr int kX = kF16 ? 2 * kXPart : kXPart;  // one X stage
+  static constexpr int kW = kF16 ? 0 : RBN * 128;        // one super-step of raw weights: 32 KB
+  static constexpr int kS = kF16 ? 0 : RBN * KS * 4;     // its (scale, zero) words: 8 KB / 4 KB
   static constexpr int kWOff = kXStages * kX;  // two weight buffers follow the X stages
   static constexpr int kSOff = kWOff + 2 * kW;
-  static constexpr int kBytes = kSOff + 2 * kS;  // 144 KB / 136 KB
-  static constexpr int kXCopies = kRingRows / 16;  // copies per wave per X stage
+  static constexpr int kBytes = kSOff + 2 * kS;  // 144 KB / 136 KB / 128 KB
+  // copies per wave per X stage (FP16: X and weights)
+  static constexpr int kXCopies = (kF16 ? 2 : 1) * (kRingRows / 16);
   // per wave per super-step: weights (8 rows per copy), scale words
-  static constexpr int kWCopies = kRingRows / 8 + kRingRows * KS / 64;
+  static constexpr int kWCopies = kF16 ? 0 : kRingRows / 8 + kRingRows * KS / 64;
 };
 
 // Global -> LDS copy of 16 (4) bytes per lane: lane l's bytes land at
@@ -341,6 +346,20 @@ __device__ __forceinline__ void x_issue(lds8* xs, const uint16_t* __restrict__ X
     const int p = (lane & 3) ^ ((row >> 1) & 3);  // global piece held by LDS slot lane & 3
     const int m = min(m0 + row, M - 1);
     copy16s(X, 2u * ((uint32_t)m * K + kb * RBK + 8 * p), xs + r0 * 64);
+  }
+}
+
+// FP16 weights of K step kb (64 bytes of each of the workgroup's 256 rows)
+// into the second half of an X stage, laid out like X.
+__device__ __forceinline__ void w16_issue(lds8* xs, const uint8_t* __restrict__ W, int N, int K,
+                                          int n0, int kb, int wave, int lane) {
+#pragma unroll
+  for (int q = 0; q < kRingRows / 16; ++q) {
+    const int r0 = kRingRows * wave + 16 * q;
+    const int row = r0 + (lane >> 2);
+    const int p = (lane & 3) ^ ((row >> 1) & 3);
+    const uint32_t n = min(n0 + row, N - 1);
+    copy16s(W, 2u * (n * (uint32_t)K + kb * RBK + 8 * p), xs + RBM * RBK * 2 + r0 * 64);
   }
 }
 
@@ -513,14 +532,22 @@ struct RingSeg {
   __device__ __forceinline__ lds8* sbuf(int s) const { return ring + R::kSOff + (s & 1) * R::kS; }
 
   __device__ __forceinline__ void issue_x(int i) {
-    x_issue(xst(i), X, M, K, m0, kb0 + min(i, nk - 1), wave, lane);
+    const int kb = kb0 + min(i, nk - 1);
+    x_issue(xst(i), X, M, K, m0, kb, wave, lane);
+    if constexpr (R::kF16) w16_issue(xst(i), W, N, K, n0, kb, wave, lane);
   }
   __device__ __forceinline__ void issue_w(int s) {
-    w_issue<WBITS>(wbuf(s), sbuf(s), W, SZ, N, K, n0, kb0 + s * KS, wave, lane);
+    if constexpr (!R::kF16)
+      w_issue<WBITS>(wbuf(s), sbuf(s), W, SZ, N, K, n0, kb0 + s * KS, wave, lane);
+  }
+  // FP16 B fragment j of step i: read like an X fragment (rows wn + 16 j + c)
+  __device__ __forceinline__ h8_t b16(int i, int j) const {
+    return lds_ld<h8_t>(xst(i) + R::kXPart + xoff + wn * 64 + 1024 * j);
   }
 
   // B fragments of step i (raw reads): position i % KS of super-step i / KS
   __device__ __forceinline__ void load_b(int i, BRaw<WBITS>& r) const {
+    if constexpr (R::kF16) return;
     const int s = i / KS, pos = i % KS;
     const lds8* wb = wbuf(s);
     const lds8* sb = sbuf(s) + 4 * pos;
@@ -570,9 +597,13 @@ struct RingSeg {
       for (int j = 0; j < 4; ++j)
         acc[i8][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i8], bf[j], acc[i8][j], 0, 0, 0);
       af[i8] = lds_ld<h8_t>(xn + 1024 * i8);
-      bw[i8 >> 2][i8 & 3] = dq_pair<WBITS>(rb1, i8 >> 2, i8 & 3, nz, sc);
-      // consumed here, so that the pair is computed inside its group
-      asm volatile("" ::"v"(bw[i8 >> 2][i8 & 3]));
+      if constexpr (R::kF16) {  // the next step's fragment j = i8 (groups 0-3)
+        if (i8 < 4) bw[i8] = __builtin_bit_cast(u4_t, b16(i + 1, i8));
+      } else {
+        bw[i8 >> 2][i8 & 3] = dq_pair<WBITS>(rb1, i8 >> 2, i8 & 3, nz, sc);
+        // consumed here, so that the pair is computed inside its group
+        asm volatile("" ::"v"(bw[i8 >> 2][i8 & 3]));
+      }
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -610,12 +641,15 @@ struct RingSeg {
 #pragma unroll
     for (int i8 = 0; i8 < 16; ++i8) af[i8] = lds_ld<h8_t>(xst(0) + xoff + 1024 * i8);
     BRaw<WBITS> rb1;
-    {
+    if constexpr (R::kF16) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = b16(0, j);
+    } else {
       BRaw<WBITS> r0;
       load_b(0, r0);
       frag_dequant<WBITS>(r0, bf);
+      load_b(1, rb1);  // step 1 is in super-step 0 (KS >= 4)
     }
-    load_b(1, rb1);  // step 1 is in super-step 0 (KS >= 4)
     for (int i = 0; i < nk; ++i) step(i, acc, af, bf, rb1);
     wait_copies<0>();  // no copy may land after the ring is reused or released
     ring_barrier();    // every wave's last fragment reads done before the next segment
@@ -1135,7 +1169,7 @@ int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* 
 // The ring kernel addresses X, W and the scale words with 32-bit byte offsets.
 bool gemm_ring_ok(int64_t M, int64_t N, int64_t K, int wbits) {
   const int64_t lim = (int64_t)1 << 32;
-  return M >= RBM && wbits != 16 && M * K * 2 < lim && N * K * wbits / 8 < lim &&
+  return M >= RBM && M * K * 2 < lim && N * K * wbits / 8 < lim &&
          N * (K / 32) * 4 < lim;
 }
 
@@ -1162,8 +1196,11 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
   // whole rounds of 256 workgroups, the last one to two rounds' tiles are
   // shared out by stream-K (at least a whole tile's work per workgroup when
   // there are more tiles than CUs, so that a tile is cut at most twice).
+  // Whole tiles when their rounds are at least 7/8 full: the partials and
+  // their reduce then cost what the idle CUs would (the LM head of a
+  // 512-token prompt, 1188 tiles in 5 rounds: 1109 us whole, 1116 us shared).
   const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
-  const int KS = wbits == 4 ? Ring<4>::KS : Ring<8>::KS;
+  const int KS = wbits == 4 ? Ring<4>::KS : wbits == 8 ? Ring<8>::KS : Ring<16>::KS;
   RingPlan pl;
   pl.U = (int)((K / RBK + KS - 1) / KS);
   int64_t dp = tiles, sk = 0;
@@ -1171,7 +1208,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
   if (v >= 2) {                                // about v segments per tile, all tiles shared
     dp = 0;
     sk = std::min<int64_t>(tiles * v, tiles * pl.U);
-  } else if (v == 1 || tiles % kRingCUs == 0) {
+  } else if (v == 1 || 8 * tiles >= 7 * kRingCUs * ((tiles + kRingCUs - 1) / kRingCUs)) {
     dp = tiles;
   } else if (tiles > kRingCUs) {
     dp = (tiles / kRingCUs - 1) * kRingCUs;
@@ -1220,9 +1257,12 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
     if (wbits == 4)
       hipLaunchKernelGGL(gemm_ring_kernel<4>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
                          yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U, pl.maxseg);
-    else
+    else if (wbits == 8)
       hipLaunchKernelGGL(gemm_ring_kernel<8>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
                          yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U, pl.maxseg);
+    else
+      hipLaunchKernelGGL(gemm_ring_kernel<16>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp,
+                         sp, yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U, pl.maxseg);
     R4Q_TRY(launch_status("gemm_ring"));
     if (pl.ws) {
       const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);

@@ -105,7 +105,9 @@ def test_gemm_workspace_sizes():
     projections at M = 8 take the split counts measured fastest); the FP16 LM
     head (2374 tiles, over 8 workgroups per CU once split), one row, and
     shapes off the ring's K step ask for none; M >= 256 follows the tiled
-    GEMM's plan."""
+    GEMM's plan: stream-K partials when the 256 x 256 tiles leave CUs idle,
+    none when the tiles fill their rounds of 256 workgroups to 7/8 or more
+    (the FP16 LM head of a 512-token prompt: 1188 tiles in 5 rounds)."""
     def ws(M, N, K, bits):
         b = C.c_size_t(123)
         R.call("r4q_gemm_workspace_bytes", M, N, K, bits, C.byref(b))
@@ -118,6 +120,9 @@ def test_gemm_workspace_sizes():
     assert ws(1, 5120, 17408, 4) == 0                 # batch 1: GEMV, no workspace
     assert ws(8, 5120, 17408 + 32, 4) == 0            # K off the ring step: per-row path
     assert ws(512, 5120, 17408, 4) > 0                # tiled GEMM, split along K
+    assert ws(512, 17408, 5120, 16) > 0               # FP16 weights: the same ring
+    assert ws(512, 151936, 5120, 16) == 0             # 1188 tiles: whole tiles
+    assert ws(2304, 16384, 768, 8) > 0                # 576 tiles: 2 rounds + stream-K
     with pytest.raises(RuntimeError):
         ws(8, 5120, 100, 4)                           # K % 32 != 0
 

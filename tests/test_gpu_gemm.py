@@ -92,7 +92,7 @@ def test_skinny_gemm_one_hot_columns_exact(dev, bits):
         assert np.array_equal(y[r], W[:, k]), k
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 8, 16])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (257, 520, 32), (600, 256, 4096),
                                    (512, 7168, 5120), (256, 255, 96)])
 def test_ring_gemm_ragged_and_split(dev, bits, M, N, K):
@@ -106,7 +106,7 @@ def test_ring_gemm_ragged_and_split(dev, bits, M, N, K):
         assert rel_l2(got[r], want[r]) <= TOL, r
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 8, 16])
 @pytest.mark.parametrize("N,K", [(700, 1024), (300, 8192)])
 def test_ring_gemm_one_hot_columns_exact(dev, bits, N, K):
     """Row r of x = e_k(r) over 300 rows: y[r] is column k(r) of the
@@ -115,12 +115,13 @@ def test_ring_gemm_one_hot_columns_exact(dev, bits, N, K):
     g = S.gen(43 + bits + K)
     M = 300
     w, sz = S.weight(N, K, bits, g)
-    W = O.dequant(w.numpy(), sz.numpy(), bits)
+    W = O.dequant(w.numpy(), None if sz is None else sz.numpy(), bits)
     ks = [(r * 997 + r // 7) % K for r in range(M)]
     x = torch.zeros(M, K, dtype=torch.float16)
     for r, k in enumerate(ks):
         x[r, k] = 1.0
-    y = int4_hip.dbg_gemm(x.to(dev), w.to(dev), sz.to(dev), M, N, K).cpu().numpy()
+    y = int4_hip.dbg_gemm(x.to(dev), w.to(dev), None if sz is None else sz.to(dev), M, N, K)
+    y = y.cpu().numpy()
     for r, k in enumerate(ks):
         assert np.array_equal(y[r], W[:, k]), (r, k)
 
@@ -217,11 +218,11 @@ def _ref32(x, w, sz, bits):
     """x @ deq(W)^T in float32 on the CPU: the oracle's dequantisation (bit-exact
     to the kernels') and a library matmul, for shapes too large for the
     float64 oracle GEMM to finish in seconds."""
-    W = torch.from_numpy(O.dequant(w.numpy(), sz.numpy(), bits)).float()
+    W = torch.from_numpy(O.dequant(w.numpy(), None if sz is None else sz.numpy(), bits)).float()
     return (x.float() @ W.T).numpy()
 
 
-@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("bits", [4, 8, 16])
 def test_ring_gemm_whole_tile_rounds_then_stream_k(dev, bits):
     """576 tiles of 256 x 256 (more than two rounds of 256 workgroups): the
     first round's tiles are computed whole, the remaining 320 tiles' K units
@@ -236,7 +237,8 @@ def test_ring_gemm_whole_tile_rounds_then_stream_k(dev, bits):
     nws = C.c_size_t(0)
     R.call("r4q_gemm_workspace_bytes", M, N, K, bits, C.byref(nws))
     assert nws.value > 0
-    got = int4_hip.dbg_gemm(x.to(dev), w.to(dev), sz.to(dev), M, N, K).float().cpu().numpy()
+    SZ = None if sz is None else sz.to(dev)
+    got = int4_hip.dbg_gemm(x.to(dev), w.to(dev), SZ, M, N, K).float().cpu().numpy()
     want = _ref32(x, w, sz, bits)
     assert np.all(np.isfinite(got))
     assert rel_l2(got, want) <= TOL
