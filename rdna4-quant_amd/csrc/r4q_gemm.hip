@@ -176,6 +176,18 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint16_t* __restri
     }
 }
 
+// (1024 + q_2p, 1024 + q_2p+1) as an fp16 pair from byte p of a packed INT4
+// word w (w4 = w >> 4): v_perm puts byte p of w in byte 0 and byte p of w4 in
+// byte 2, one v_and_or keeps the low nibbles and sets the 0x64 exponent bytes
+// (written out: with two literal operands, which VOP3 cannot encode on this
+// target, the compiler emits a separate AND and OR).
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, uint32_t w4, int p) {
+  const uint32_t t = __builtin_amdgcn_perm(w4, w, (uint32_t)(p | (p + 4) << 16));
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(t), "s"(0x000F000Fu), "v"(0x64006400u));
+  return r;
+}
+
 // ---------------------------------------------------------------------
 // Weight fragments of the skinny GEMM (below).  The MFMA contraction index k
 // is only a label: lane group g's 8 k-slots of an MFMA carry 8 weight
@@ -184,9 +196,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(const uint16_t* __restri
 // dequantised before the MFMA -- fp16((q - zp) * s) by an exact packed fp16
 // subtraction and one rounded packed multiply, bit-identical to the dequant
 // kernel -- the accumulation may run across blocks.
-//   INT4: 4 MFMAs per 16 weight bytes; nibble pairs (q_p, q_p+4) come from
-//         (w >> 4p) & 0x000F000F | 0x64006400, so the activation is permuted
-//         to (x_p, x_p+4) pairs;
+//   INT4: 4 MFMAs per 16 weight bytes; the nibble pair (q_2j, q_2j+1) of
+//         byte j of a word w is byte j of w and of w >> 4 (v_perm), masked
+//         and tagged 0x6400 in one v_and_or: natural k order, so the
+//         activation is used as loaded;
 //   INT8: 2 MFMAs per 16 bytes; byte pairs by v_perm, natural order;
 //   FP16: 1 MFMA per 16 bytes.
 // B fragment of MFMA d from 16 weight bytes w and the block's (scale, zero) s2.
@@ -202,9 +215,9 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
     const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));
     uint32_t pr[4];
     if constexpr (WBITS == 4) {
-      const uint32_t wd = w[d];
+      const uint32_t wd = w[d], wd4 = wd >> 4;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) pr[p] = ((wd >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
+      for (int p = 0; p < 4; ++p) pr[p] = nib_pair(wd, wd4, p);
     } else {
       const uint32_t w0 = w[2 * d], w1 = w[2 * d + 1];
       pr[0] = __builtin_amdgcn_perm(w0, 0x64646464u, 0x00050004u);
@@ -426,16 +439,9 @@ __device__ __forceinline__ void frag_dequant(const BRaw<WBITS>& r, h8_t* bf) {
     const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
     uint32_t pr[4];  // (1024 + q_2k, 1024 + q_2k+1) as fp16 pairs
     if constexpr (WBITS == 4) {
-      typedef uint16_t us2 __attribute__((ext_vector_type(2)));
-      const us2 sh = {0, 4};
+      const uint32_t w4 = r.w[j][0] >> 4;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        // byte k in both halves, the high half shifted down by 4
-        const uint32_t tb =
-            __builtin_amdgcn_perm(0u, r.w[j][0], (k | 0x0C00u | (k << 16) | 0x0C000000u));
-        const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
-        pr[k] = (nib & 0x000F000Fu) | 0x64006400u;
-      }
+      for (int k = 0; k < 4; ++k) pr[k] = nib_pair(r.w[j][0], w4, k);
     } else {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
@@ -451,24 +457,21 @@ __device__ __forceinline__ void frag_dequant(const BRaw<WBITS>& r, h8_t* bf) {
 
 // Pair k (k labels 8g + 2k, 8g + 2k + 1) of B fragment j, the same
 // arithmetic as frag_dequant, so that the dequantisation can be spread over
-// a step's MFMAs one pair at a time.  nz / sc: fragment j's -(1024 + zp)
-// and scale pairs (set by the pair-0 call).
+// a step's MFMAs one pair at a time.  nz / sc / w4: fragment j's
+// -(1024 + zp) and scale pairs and (INT4) its word shifted by 4, set by the
+// pair-0 call.
 template <int WBITS>
 __device__ __forceinline__ uint32_t dq_pair(const BRaw<WBITS>& r, int j, int k, h2_t& nz,
-                                            h2_t& sc) {
+                                            h2_t& sc, uint32_t& w4) {
   if (k == 0) {
     const uint32_t sb = r.s2[j] & 0xFFFFu, zb = r.s2[j] >> 16;
     sc = as_h2(sb | (sb << 16));
     nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
+    if constexpr (WBITS == 4) w4 = r.w[j][0] >> 4;
   }
   uint32_t pr;
   if constexpr (WBITS == 4) {
-    typedef uint16_t us2 __attribute__((ext_vector_type(2)));
-    const us2 sh = {0, 4};
-    const uint32_t tb =
-        __builtin_amdgcn_perm(0u, r.w[j][0], (k | 0x0C00u | (k << 16) | 0x0C000000u));
-    const uint32_t nib = __builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, tb) >> sh);
-    pr = (nib & 0x000F000Fu) | 0x64006400u;
+    pr = nib_pair(r.w[j][0], w4, k);
   } else {
     pr = __builtin_amdgcn_perm(r.w[j][k >> 1], 0x64646464u, (k & 1) ? 0x00070006u : 0x00050004u);
   }
@@ -590,6 +593,7 @@ struct RingSeg {
     // fragment, and pair i8 % 4 of the next step's B fragment i8 / 4
     u4_t bw[4];
     h2_t nz, sc;
+    uint32_t w4 = 0;
     const lds8* xn = xst(i + 1) + xoff;
 #pragma unroll
     for (int i8 = 0; i8 < 16; ++i8) {
@@ -600,7 +604,7 @@ struct RingSeg {
       if constexpr (R::kF16) {  // the next step's fragment j = i8 (groups 0-3)
         if (i8 < 4) bw[i8] = __builtin_bit_cast(u4_t, b16(i + 1, i8));
       } else {
-        bw[i8 >> 2][i8 & 3] = dq_pair<WBITS>(rb1, i8 >> 2, i8 & 3, nz, sc);
+        bw[i8 >> 2][i8 & 3] = dq_pair<WBITS>(rb1, i8 >> 2, i8 & 3, nz, sc, w4);
         // consumed here, so that the pair is computed inside its group
         asm volatile("" ::"v"(bw[i8 >> 2][i8 & 3]));
       }
@@ -871,51 +875,132 @@ struct SkRing {
   static_assert(kX % (kX16 ? 4096 : 1024) == 0 && kCX >= 1, "activation copies must split evenly");
 };
 
-// Copies step kb of the workgroup's weight rows, scales and activation rows
-// into ring stage `stage` (rows past N / M clamped to the last one).
+// Per-lane source offsets of the copies of one ring step (bytes from the
+// step's uniform bases W + 128 kb, SZ + kb * words, X + kb * kKS; rows past N /
+// M clamped to the last one), computed once per workgroup: a step's copies
+// then cost no vector arithmetic.
 template <int WBITS, int MR>
-__device__ __forceinline__ void sk_issue(uint8_t* stage, const uint16_t* __restrict__ X,
-                                         const uint8_t* __restrict__ W,
-                                         const uint32_t* __restrict__ SZ, int M, int N, int K,
-                                         int n0, int kb, int wave, int lane) {
+struct SkCopy {
   using R = SkRing<WBITS, MR>;
-  const int64_t row_bytes = (int64_t)K * WBITS / 8;
+  static constexpr int kWpr = R::kSRow / 4;  // scale words per row per step
+  uint32_t wo[2], so[R::kCS > 0 ? R::kCS : 1], xo[R::kCX];
+
+  __device__ __forceinline__ void init(int M, int N, int K, int n0, int wave, int lane) {
+    const uint32_t row_bytes = (uint32_t)K * WBITS / 8;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {  // weights: copy c covers tile rows 8c .. 8c+7
-    const int c = 2 * wave + i, r = 8 * c + (lane >> 3);
-    const int piece = (lane & 7) ^ (r & 7);
-    const int64_t n = min(n0 + r, N - 1);
-    copy16(W + n * row_bytes + (int64_t)kb * 128 + 16 * piece, stage + 1024 * c);
-  }
-  if constexpr (WBITS != 16) {
-    const int nb = K / 32;
-    constexpr int wpr = R::kSRow / 4;   // scale words per row per step
-    constexpr int rpc = 64 / wpr;       // rows per 256-byte copy
+    for (int i = 0; i < 2; ++i) {  // weights: copy c covers tile rows 8c .. 8c+7
+      const int c = 2 * wave + i, r = 8 * c + (lane >> 3);
+      const int piece = (lane & 7) ^ (r & 7);
+      wo[i] = (uint32_t)min(n0 + r, N - 1) * row_bytes + 16 * piece;
+    }
+    if constexpr (WBITS != 16) {
+      constexpr int rpc = 64 / kWpr;  // rows per 256-byte copy
 #pragma unroll
-    for (int i = 0; i < R::kCS; ++i) {
-      const int c = R::kCS * wave + i, r = rpc * c + lane / wpr;
-      const int64_t n = min(n0 + r, N - 1);
-      copy4(SZ + n * nb + (int64_t)kb * wpr + lane % wpr, stage + R::kW + 256 * c);
+      for (int i = 0; i < R::kCS; ++i) {
+        const int c = R::kCS * wave + i, r = rpc * c + lane / kWpr;
+        so[i] = 4u * ((uint32_t)min(n0 + r, N - 1) * (uint32_t)(K / 32) + lane % kWpr);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R::kCX; ++i) {
+      const int c = R::kCX * wave + i;
+      if constexpr (R::kX16) {  // 1 KB per copy, 16 bytes per lane
+        const int off = 1024 * c + 16 * lane;
+        const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
+        xo[i] = 2u * ((uint32_t)min(r, M - 1) * K + 8 * (slot ^ (r & 7)));
+      } else {  // 256 B per copy, 4 bytes per lane
+        const int off = 256 * c + 4 * lane;
+        const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
+        xo[i] = 2u * ((uint32_t)min(r, M - 1) * K + 8 * (slot ^ (r & 7)) + 2 * (lane & 3));
+      }
     }
   }
-  const uint16_t* xs = X + (int64_t)kb * R::kKS;
+
+  // step kb of the workgroup's weight rows, scale words and activation rows
+  // into ring stage `stage`
+  __device__ __forceinline__ void issue(lds8* stage, const uint16_t* __restrict__ X,
+                                        const uint8_t* __restrict__ W,
+                                        const uint32_t* __restrict__ SZ, int kb,
+                                        int wave) const {
+    const uint8_t* wb = W + (int64_t)kb * 128;
 #pragma unroll
-  for (int i = 0; i < R::kCX; ++i) {
-    const int c = R::kCX * wave + i;
-    if constexpr (R::kX16) {  // 1 KB per copy, 16 bytes per lane
-      const int off = 1024 * c + 16 * lane;
-      const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
-      const int64_t m = min(r, M - 1);
-      copy16(xs + m * K + 8 * (slot ^ (r & 7)), stage + R::kW + R::kS + 1024 * c);
-    } else {  // 256 B per copy, 4 bytes per lane
-      const int off = 256 * c + 4 * lane;
-      const int r = off / R::kXRow, slot = (off % R::kXRow) / 16;
-      const int64_t m = min(r, M - 1);
-      copy4(xs + m * K + 8 * (slot ^ (r & 7)) + 2 * (lane & 3),
-            stage + R::kW + R::kS + 256 * c);
+    for (int i = 0; i < 2; ++i) copy16s(wb, wo[i], stage + 1024 * (2 * wave + i));
+    if constexpr (WBITS != 16) {
+      const uint32_t* sb = SZ + (int64_t)kb * kWpr;
+#pragma unroll
+      for (int i = 0; i < R::kCS; ++i) copy4s(sb, so[i], stage + R::kW + 256 * (R::kCS * wave + i));
+    }
+    const uint16_t* xs = X + (int64_t)kb * R::kKS;
+#pragma unroll
+    for (int i = 0; i < R::kCX; ++i) {
+      const int c = R::kCX * wave + i;
+      if constexpr (R::kX16) copy16s(xs, xo[i], stage + R::kW + R::kS + 1024 * c);
+      else copy4s(xs, xo[i], stage + R::kW + R::kS + 256 * c);
     }
   }
-}
+};
+
+// The K loop of one workgroup.  The ring stage of a step is a template
+// argument (the loop is unrolled by the ring depth), so that the LDS reads
+// address each stage through their immediate offset from per-lane offsets
+// computed once.
+template <int WBITS, int MR>
+struct SkLoop {
+  using R = SkRing<WBITS, MR>;
+  static constexpr int D = kSkStages;
+  lds8* ring;
+  const uint16_t* X;
+  const uint8_t* W;
+  const uint32_t* SZ;
+  SkCopy<WBITS, MR> cp;
+  int kb0, nk, wave;
+  uint32_t ob0, ob1, osw, ox[R::kSteps];  // per-lane LDS offsets within a stage
+  f4_t acc;
+
+  template <int ST>
+  __device__ __forceinline__ void step(int i) {
+    wait_copies<(D - 2) * R::kPer>();  // this wave's copies of step i have landed
+    ring_barrier();                    // every wave's; every wave is done with step i-1
+    cp.issue(ring + ((ST + D - 1) % D) * R::kStage, X, W, SZ, kb0 + min(i + D - 1, nk - 1),
+             wave);
+    const lds8* st = ring + ST * R::kStage;
+    const u4_t b0 = lds_ld<u4_t>(st + ob0);
+    const u4_t b1 = lds_ld<u4_t>(st + ob1);
+    uint32_t sw0 = 0u, sw1 = 0u;
+    if constexpr (WBITS == 4) {  // blocks 2g, 2g+1 of the step
+      const u2_t v = lds_ld<u2_t>(st + osw);
+      sw0 = v[0];
+      sw1 = v[1];
+    } else if constexpr (WBITS == 8) {  // block g
+      sw0 = lds_ld<uint32_t>(st + osw);
+    }
+#pragma unroll
+    for (int j = 0; j < R::kSteps; ++j) {
+      // activation piece holding k labels k0 + (KS/4) g + 8 j .. +7
+      const h8_t a = lds_ld<h8_t>(st + ox[j]);
+      h8_t b;
+      if constexpr (WBITS == 4) b = skinny_b<4>(j < 4 ? b0 : b1, j < 4 ? sw0 : sw1, j & 3);
+      else if constexpr (WBITS == 8) b = skinny_b<8>(j < 2 ? b0 : b1, sw0, j & 1);
+      else b = __builtin_bit_cast(h8_t, j == 0 ? b0 : b1);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    }
+  }
+
+  __device__ __forceinline__ void run() {
+#pragma unroll
+    for (int s = 0; s < D - 1; ++s)
+      cp.issue(ring + s * R::kStage, X, W, SZ, kb0 + min(s, nk - 1), wave);
+    static_assert(D == 3, "the loop below is unrolled by the ring depth");
+    int i = 0;
+    for (; i + 3 <= nk; i += 3) {
+      step<0>(i);
+      step<1>(i + 1);
+      step<2>(i + 2);
+    }
+    if (i < nk) step<0>(i);
+    if (i + 1 < nk) step<1>(i + 1);
+  }
+};
 
 template <int WBITS, int MR>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
@@ -925,64 +1010,34 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
                                                           float* __restrict__ part, int M, int N,
                                                           int K, int ntiles, int kps) {
   using R = SkRing<WBITS, MR>;
-  constexpr int D = kSkStages;
-  __shared__ __align__(16) uint8_t ring[D * R::kStage];
+  __shared__ __align__(16) uint8_t ring[kSkStages * R::kStage];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
   const int n0 = tile * kSkTile;
   const int kt = K / R::kKS;
-  const int kb0 = sp * kps, nk = min(kt - kb0, kps);  // >= 1 (host)
   const int col = lane & 15, g = lane >> 4;
   const int wrow = 16 * wave + col;                   // this lane's weight row in the tile
   const int xr = col % MR;                            // activation row (rows >= MR: duplicates)
 
-  f4_t acc = f4_t{0.f, 0.f, 0.f, 0.f};
+  SkLoop<WBITS, MR> lp;
+  lp.ring = (lds8*)ring;
+  lp.X = X;
+  lp.W = W;
+  lp.SZ = SZ;
+  lp.kb0 = sp * kps;
+  lp.nk = min(kt - lp.kb0, kps);  // >= 1 (host)
+  lp.wave = wave;
+  lp.cp.init(M, N, K, n0, wave, lane);
+  // weight bytes [32 g, 32 g + 32) of row wrow: pieces 2g, 2g+1
+  lp.ob0 = 128 * wrow + 16 * ((2 * g) ^ (wrow & 7));
+  lp.ob1 = 128 * wrow + 16 * ((2 * g + 1) ^ (wrow & 7));
+  lp.osw = R::kW + R::kSRow * wrow + (WBITS == 4 ? 8 * g : 4 * g);
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s)
-    sk_issue<WBITS, MR>(ring + s * R::kStage, X, W, SZ, M, N, K, n0, kb0 + min(s, nk - 1), wave,
-                        lane);
-  for (int i = 0; i < nk; ++i) {
-    wait_copies<(D - 2) * R::kPer>();  // this wave's copies of step i have landed
-    ring_barrier();                    // every wave's; every wave is done with step i-1
-    sk_issue<WBITS, MR>(ring + ((i + D - 1) % D) * R::kStage, X, W, SZ, M, N, K, n0,
-                        kb0 + min(i + D - 1, nk - 1), wave, lane);
-    const uint8_t* st = ring + (i % D) * R::kStage;
-    // weight bytes [32 g, 32 g + 32) of row wrow: pieces 2g, 2g+1
-    const u4_t b0 = *reinterpret_cast<const u4_t*>(st + 128 * wrow + 16 * ((2 * g) ^ (wrow & 7)));
-    const u4_t b1 =
-        *reinterpret_cast<const u4_t*>(st + 128 * wrow + 16 * ((2 * g + 1) ^ (wrow & 7)));
-    uint32_t sw0 = 0u, sw1 = 0u;
-    if constexpr (WBITS == 4) {  // blocks 2g, 2g+1 of the step
-      const uint2 v = *reinterpret_cast<const uint2*>(st + R::kW + R::kSRow * wrow + 8 * g);
-      sw0 = v.x;
-      sw1 = v.y;
-    } else if constexpr (WBITS == 8) {  // block g
-      sw0 = *reinterpret_cast<const uint32_t*>(st + R::kW + R::kSRow * wrow + 4 * g);
-    }
-    const uint8_t* xst = st + R::kW + R::kS + R::kXRow * xr;
-#pragma unroll
-    for (int j = 0; j < R::kSteps; ++j) {
-      // activation piece holding k labels k0 + (KS/4) g + 8 j .. +7
-      const int piece = (R::kKS / 32) * g + j;
-      const u4_t av = *reinterpret_cast<const u4_t*>(xst + 16 * (piece ^ (xr & 7)));
-      h8_t a;
-      if constexpr (WBITS == 4) {  // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
-        u4_t o;
-        o[0] = (av[0] & 0xFFFFu) | (av[2] << 16);
-        o[1] = (av[0] >> 16) | (av[2] & 0xFFFF0000u);
-        o[2] = (av[1] & 0xFFFFu) | (av[3] << 16);
-        o[3] = (av[1] >> 16) | (av[3] & 0xFFFF0000u);
-        a = __builtin_bit_cast(h8_t, o);
-      } else {
-        a = __builtin_bit_cast(h8_t, av);
-      }
-      h8_t b;
-      if constexpr (WBITS == 4) b = skinny_b<4>(j < 4 ? b0 : b1, j < 4 ? sw0 : sw1, j & 3);
-      else if constexpr (WBITS == 8) b = skinny_b<8>(j < 2 ? b0 : b1, sw0, j & 1);
-      else b = __builtin_bit_cast(h8_t, j == 0 ? b0 : b1);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
-    }
-  }
+  for (int j = 0; j < R::kSteps; ++j)
+    lp.ox[j] = R::kW + R::kS + R::kXRow * xr + 16 * ((R::kSteps * g + j) ^ (xr & 7));
+  lp.acc = f4_t{0.f, 0.f, 0.f, 0.f};
+  lp.run();
+  const f4_t acc = lp.acc;
   wait_copies<0>();  // no copy into LDS outlives the workgroup
   // C: lane holds activation rows 4g + r, weight row n0 + 16 wave + col
   const int n = n0 + 16 * wave + col;
@@ -1056,9 +1111,10 @@ __global__ __launch_bounds__(64) void gemm_skinny_reduce_silu_kernel(
 
 }  // namespace
 
-bool gemm_skinny_ok(int64_t M, int64_t K, int wbits) {
+bool gemm_skinny_ok(int64_t M, int64_t N, int64_t K, int wbits) {
   const int64_t ks = 1024 / (wbits == 4 ? 4 : wbits == 8 ? 8 : 16);  // k per ring step
-  return M >= 2 && M <= 16 && K % ks == 0;
+  // the copies address the weights with 32-bit byte offsets
+  return M >= 2 && M <= 16 && K % ks == 0 && N * K * wbits / 8 < ((int64_t)1 << 32);
 }
 
 // Split count of the skinny ring.  A CU streams its workgroups' weight
@@ -1154,7 +1210,7 @@ int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, in
 }
 
 bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes) {
-  return gemm_skinny_ok(M, K, wbits) && I > 0 && I % 32 == 0 &&
+  return gemm_skinny_ok(M, 2 * I, K, wbits) && I > 0 && I % 32 == 0 &&
          skinny_splits(M, 2 * I, K, wbits, ws_bytes) > 1;
 }
 

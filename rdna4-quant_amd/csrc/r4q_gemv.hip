@@ -886,13 +886,13 @@ bool gemv_silu_ok(int64_t N, int64_t K, int wbits) {
 
 size_t gemm_ws_need(int64_t M, int64_t N, int64_t K, int wbits) {
   if (M > kSkinnyMaxRows) return gemm_ws_bytes(M, N, K, wbits);
-  return gemm_skinny_ok(M, K, wbits) ? skinny_ws_bytes(M, N, K, wbits) : 0;
+  return gemm_skinny_ok(M, N, K, wbits) ? skinny_ws_bytes(M, N, K, wbits) : 0;
 }
 
 int gemm_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                 int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes) {
   if (M > kSkinnyMaxRows) return gemm_mfma_launch(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes);
-  if (gemm_skinny_ok(M, K, wbits))
+  if (gemm_skinny_ok(M, N, K, wbits))
     return gemm_skinny_launch(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes);
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* yp = static_cast<uint16_t*>(y);

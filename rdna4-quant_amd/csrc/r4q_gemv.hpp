@@ -55,9 +55,9 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
                      size_t ws_bytes = 0);
 
 // Skinny MFMA GEMM for 2 <= M <= 16 rows (weights streamed once); usable
-// when gemm_skinny_ok(M, K, wbits).  With a workspace of at least
+// when gemm_skinny_ok(M, N, K, wbits).  With a workspace of at least
 // skinny_ws_bytes() narrow shapes are split along K (fp32 partials).
-bool gemm_skinny_ok(int64_t M, int64_t K, int wbits);
+bool gemm_skinny_ok(int64_t M, int64_t N, int64_t K, int wbits);
 size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits);
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                        int64_t N, int64_t K, int wbits, hipStream_t st, void* ws = nullptr,
