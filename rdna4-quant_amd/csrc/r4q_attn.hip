@@ -161,19 +161,28 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   const bool owner = NORMQ && (pos >> 5) % nsplit == sp;  // holds the new position's chunk
   const int ntask = G + (owner ? 2 : 0);
   uint16_t px[kSlots][2], pw[kSlots][2];  // raw fp16, widened after the KV loads issue
+  float pf[NORMQ ? kSlots : 1][2][kMaxQkvSplits];  // split partials (qk.nsum >= 2)
   uint16_t pc = 0, ps = 0;
   if constexpr (NORMQ) {
-    const uint16_t* row = q + b * q_stride;  // raw QKV row: q | k | v heads
     // branch-free, so that all of them are in flight together (slots past
     // the wave's tasks read head 0 and are not used)
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const int task = wave + 4 * i;
       const int head = task >= ntask ? 0 : task < G ? kh * G + task : task == G ? H + kh : H + Hk + kh;
-      const uint16_t* src = row + (int64_t)head * 128;
+      const int64_t off = b * q_stride + (int64_t)head * 128;  // raw QKV row: q | k | v heads
+      if (qk.nsum >= 2) {  // wave-uniform
+#pragma unroll
+        for (int z = 0; z < kMaxQkvSplits; ++z) {
+          const float* src = qk.part + min(z, qk.nsum - 1) * qk.plane + off;
+          pf[i][0][z] = src[lane];
+          pf[i][1][z] = src[lane + 64];
+        }
+      } else {
+        px[i][0] = q[off + lane];
+        px[i][1] = q[off + lane + 64];
+      }
       const uint16_t* w = task < G ? qk.qw : qk.kw;
-      px[i][0] = src[lane];
-      px[i][1] = src[lane + 64];
       pw[i][0] = w[lane];
       pw[i][1] = w[lane + 64];
     }
@@ -196,6 +205,18 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // widened in straight-line code: every slot's loads are consumed here,
     // before any branch (none is sunk behind the KV loads)
     const float c = h2f_ieee(pc), sn = h2f_ieee(ps);
+    if (qk.nsum >= 2) {  // the split reduce's sum, in split order, rounded to fp16
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float v = pf[i][e][0];
+#pragma unroll
+          for (int z = 1; z < kMaxQkvSplits; ++z)
+            if (z < qk.nsum) v += pf[i][e][z];
+          px[i][e] = f2h(v);
+        }
+    }
     float fx[kSlots][2], fw[kSlots][2];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {

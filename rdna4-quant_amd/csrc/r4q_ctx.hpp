@@ -62,7 +62,13 @@ struct AttnQK {
   uint8_t* kc;         // caches to write at position L-1
   uint8_t* vc;
   float eps;
+  // nsum >= 2: the raw QKV rows are the split sums fp16(sum over s < nsum of
+  // part[s * plane + row offset]) of a split-K projection (nsum <= kMaxQkvSplits)
+  const float* part = nullptr;
+  int64_t plane = 0;
+  int nsum = 0;
 };
+constexpr int kMaxQkvSplits = 4;
 
 // qk == nullptr: q rows are final (normed, rotated) queries.  Otherwise q
 // rows are raw QKV projection rows and the fused prologue above runs.

@@ -211,6 +211,15 @@ struct Prof {
 // Enqueues one decode step for B rows.  pos_dev/seq_dev: device-held
 // position and length (graph replay), else pos_host.  Input hidden states
 // must already be in bf.h.
+// Batched steps (B > 1): the qkv projection's K split partials are summed by
+// the attention prologue when the skinny GEMM splits K into 2..kMaxQkvSplits.
+bool qkv_partials_in_attention(int64_t B, const Dims& dm, int bits, size_t ws_bytes) {
+  if (B == 1 || tuning().qkv_reduce.load() != 0 || !gemm_skinny_ok(B, dm.qkvN, dm.D, bits))
+    return false;
+  const int S = skinny_splits(B, dm.qkvN, dm.D, bits, ws_bytes);
+  return S >= 2 && S <= kMaxQkvSplits;
+}
+
 int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host,
                  const int* pos_dev, const int* seq_dev, int nsplit, const Bufs& bf, bool logits,
                  hipStream_t st, Prof prof = Prof()) {
@@ -228,7 +237,13 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
   for (int li = 0; li < dm.L; ++li) {
     const r4q_layer& y = m->layers[li];
     prof.mark(st, kGemv);
-    if (!fused) {
+    // batches: a split-K skinny qkv projection leaves its fp32 partials for
+    // the attention prologue to sum (no reduce launch)
+    int qkv_nsum = 0;
+    if (!fused && qkv_partials_in_attention(B, dm, y.qkv_bits, bf.ws_bytes)) {
+      R4Q_TRY(gemm_skinny_part_launch(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D,
+                                      y.qkv_bits, st, bf.ws, bf.ws_bytes, &qkv_nsum));
+    } else if (!fused) {
       R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st, bf));
     } else if (li == 0) {  // input hidden state: plain RMSNorm
       R4Q_TRY(gemv_norm_launch(bf.h, nullptr, y.in_norm, nullptr, eps, y.qkv_w, y.qkv_s, bf.qkv,
@@ -243,7 +258,9 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     const AttnQK qk{static_cast<const uint16_t*>(y.q_norm), static_cast<const uint16_t*>(y.k_norm),
                     static_cast<const uint16_t*>(m->rope_cos),
                     static_cast<const uint16_t*>(m->rope_sin), static_cast<uint8_t*>(y.k_cache),
-                    static_cast<uint8_t*>(y.v_cache), eps};
+                    static_cast<uint8_t*>(y.v_cache), eps,
+                    qkv_nsum >= 2 ? static_cast<const float*>(bf.ws) : nullptr,
+                    B * dm.qkvN, qkv_nsum >= 2 ? qkv_nsum : 0};
     R4Q_TRY(launch_flash_decode(bf.qkv, dm.qkvN, y.k_cache, y.v_cache, y.k_scale, y.v_scale,
                                 bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
                                 nsplit, 1, bf.attn, st, &qk));
@@ -475,8 +492,13 @@ std::vector<uint8_t> graph_key(int kind, const r4q_model* m, int64_t B, int nspl
                                const void* sample_ws) {
   const void* extra[] = {tokens_out, bf.h, bf.attn, bf.state, bf.ws, sample_ws};
   const uint64_t epoch = devbuf_epoch();
+  // launch-shape overrides change what a step launches
+  const Tuning& tu = tuning();
+  const int knobs[] = {tu.gemv_lpr.load(),      tu.gemv_wgs.load(),    tu.gemv_ub.load(),
+                       tu.attn_splits.load(),   tu.skinny_splits.load(), tu.gemm_splits.load(),
+                       tu.qkv_reduce.load()};
   std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 16 +
-                         sizeof(extra) + sizeof(epoch) + sizeof(SampleCfg));
+                         sizeof(extra) + sizeof(epoch) + sizeof(SampleCfg) + sizeof(knobs));
   uint8_t* p = k.data();
   memcpy(p, m, sizeof(r4q_model));
   p += sizeof(r4q_model);
@@ -491,6 +513,8 @@ std::vector<uint8_t> graph_key(int kind, const r4q_model* m, int64_t B, int nspl
   memcpy(p, &epoch, sizeof(epoch));
   p += sizeof(epoch);
   memcpy(p, &scfg, sizeof(SampleCfg));
+  p += sizeof(SampleCfg);
+  memcpy(p, knobs, sizeof(knobs));
   return k;
 }
 
@@ -557,14 +581,16 @@ extern "C" int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int6
   Dims dm;
   R4Q_TRY(validate(m, B, dm));
   const size_t gws = step_gemm_ws(m, dm, B);
-  int fused = 0;
+  int fused = 0, qkv_sum = 0;
   for (int li = 0; li < dm.L; ++li) {
     const int bits = m->layers[li].gu_bits;
     fused += B == 1 ? (bits != 16 && gemv_silu_ok(2 * (int64_t)dm.I, dm.D, bits))
                     : gemm_skinny_silu_ok(B, dm.I, dm.D, bits, gws);
+    qkv_sum += qkv_partials_in_attention(B, dm, m->layers[li].qkv_bits, gws);
   }
   out[0] = attn_num_splits(m->max_seq, B, dm.Hk);
   out[1] = fused;
+  if (n >= 3) out[2] = qkv_sum;
   return R4Q_OK;
 }
 

@@ -1158,8 +1158,11 @@ size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
 namespace {
 // silu_I > 0: N = 2 silu_I gate/up columns, split (S > 1, checked by the
 // caller) and reduced by gemm_skinny_reduce_silu_kernel into y (M x silu_I).
+// silu_I > 0: the reduce applies the SiLU gate; keep_part: no reduce, the S
+// fp32 partial planes stay in ws (S > 1) for the consumer to sum.
 int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
-               int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes, int64_t silu_I) {
+               int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes, int64_t silu_I,
+               bool keep_part = false) {
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
@@ -1189,6 +1192,7 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   }
 #undef R4Q_SKINNY
   R4Q_TRY(launch_status("gemm_skinny"));
+  if (keep_part) return R4Q_OK;
   if (silu_I > 0) {
     hipLaunchKernelGGL(gemm_skinny_reduce_silu_kernel,
                        dim3((unsigned)((silu_I / 32 + 63) / 64), (unsigned)M), dim3(64), 0, st,
@@ -1207,6 +1211,14 @@ int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, in
                        int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
                        size_t ws_bytes) {
   return skinny_run(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes, 0);
+}
+
+int gemm_skinny_part_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                            int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
+                            size_t ws_bytes, int* S) {
+  R4Q_REQUIRE(gemm_skinny_ok(M, N, K, wbits), "skinny GEMM: unsupported shape");
+  *S = skinny_splits(M, N, K, wbits, ws ? ws_bytes : 0);
+  return skinny_run(x, w, sz, y, M, N, K, wbits, st, ws, ws_bytes, 0, true);
 }
 
 bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes) {

@@ -59,9 +59,17 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
 // skinny_ws_bytes() narrow shapes are split along K (fp32 partials).
 bool gemm_skinny_ok(int64_t M, int64_t N, int64_t K, int wbits);
 size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits);
+// K split count the skinny GEMM takes for a shape given ws_bytes of workspace.
+int skinny_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes);
 int gemm_skinny_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                        int64_t N, int64_t K, int wbits, hipStream_t st, void* ws = nullptr,
                        size_t ws_bytes = 0);
+// The same GEMM without its split reduce: *S = the K split count; S > 1
+// leaves the S fp32 planes part[s][m][n] (part = ws) for the consumer to sum
+// in split order and round to fp16 (what the reduce stores); S == 1 writes y.
+int gemm_skinny_part_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                            int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
+                            size_t ws_bytes, int* S);
 // The same GEMM over N = 2I gate/up columns with the SiLU gate and FWHT-32
 // fused into the split sum: y (M x I fp16) = FWHT-32(silu(gate) * up),
 // equal to the plain GEMM followed by silu_mul_fwht.  Needs the split path

@@ -144,9 +144,10 @@ def oracle_step(m, hidden16, pos, kc, vc, b=0, forced_kv=None, kv_trace=None):
                          kv_trace=kv_trace)
 
 
-def plan(m, B):
+def plan(m, B, n=2):
     """r4q_decode_plan of the model: (attention split count, layers whose
-    gate/up applies the SiLU gate in the same launch)."""
+    gate/up applies the SiLU gate in the same launch[, layers whose qkv split
+    partials the attention prologue sums (n = 3)])."""
     import ctypes as C
 
     import r4q_lib as R
@@ -155,9 +156,9 @@ def plan(m, B):
     md = int4_hip.build_model(*args[:18], *args[19:], m.k_caches, m.v_caches, m.final_norm_d,
                               m.lm_w_d, m.lm_s_d, m.vocab, m.D)
     del had
-    out = (C.c_int32 * 2)()
-    R.call("r4q_decode_plan", C.byref(md.struct), B, out, 2)
-    return int(out[0]), int(out[1])
+    out = (C.c_int32 * n)()
+    R.call("r4q_decode_plan", C.byref(md.struct), B, out, n)
+    return tuple(int(v) for v in out)
 
 
 def oracle_batch_forced(m, h, pos):

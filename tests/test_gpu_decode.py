@@ -78,6 +78,36 @@ def test_qwen3_width_batch8_step_vs_oracle(dev):
         assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
 
 
+def test_qwen3_width_batch8_qkv_partials_summed_in_attention_bit_exact(dev):
+    """Batch 8 at full width: the qkv projection's split-K partials summed in
+    the attention prologue (split order, rounded to fp16) give the same
+    logits and FP8 K/V bytes, bit for bit, as the separate reduce launch
+    (qkv_reduce override), INT4 and INT8 qkv layers."""
+    import r4q_lib as R
+    bits = {(1, "qkv"): 8}
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=4096, max_seq=96, seed=14, bits=bits,
+              batch=8, fill=60, kv_scale=True)
+    assert plan(m, 8, 3)[2] == 2, "qkv partials not summed in the attention prologue"
+    h = _hidden(m, 15, rows=8).to(dev)
+    pos = 60
+    runs = []
+    for knob in (0, 1):
+        R.tune("qkv_reduce", knob)
+        try:
+            assert plan(m, 8, 3)[2] == (2 if knob == 0 else 0)
+            lg = step_logits(m, h, pos).clone()
+            kv = [gpu_kv_at(m, pos, b) for b in range(8)]
+        finally:
+            R.tune("qkv_reduce", 0)
+        runs.append((lg, kv))
+    (la, kva), (lb, kvb) = runs
+    assert torch.isfinite(la.float()).all()
+    assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
+    for b in range(8):
+        for (ka, va), (kb, vb) in zip(kva[b], kvb[b]):
+            assert np.array_equal(ka, kb) and np.array_equal(va, vb), b
+
+
 def test_qwen3_width_ctx2048_step_vs_oracle(dev):
     """Batch 1 at ctx 2048 (position 2048, cache capacity 2088): the 17-split
     attention with the head norm + RoPE + FP8 KV prologue in its owner
