@@ -334,9 +334,10 @@ R4Q_API int r4q_decode_step_graph(r4q_ctx* ctx, const r4q_model* m, const void* 
  * out[0] = attention split count (from the cache capacity),
  * out[1] = layers whose gate/up projection applies the SiLU gate + FWHT-32
  * in the same launch (batch 1: the GEMV's SiLU epilogue; batch > 1: the
- * split-K reduce of the skinny GEMM); with n >= 3, out[2] = layers whose
- * qkv split-K partials the attention prologue sums (batch > 1, no reduce
- * launch).  n >= 2. */
+ * split-K reduce of the skinny GEMM); with n >= 3, out[2] = projections
+ * (qkv, o, down over all layers) whose split-K partials are summed by the
+ * kernel consuming them -- attention prologue, row norm -- with no reduce
+ * launch (batch > 1).  n >= 2. */
 R4Q_API int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int64_t n);
 /* Run `num_tokens` steps from start_pos.  use_graph != 0 captures one step
  * into a hipGraph and replays it with the position held in device memory.
@@ -377,10 +378,11 @@ R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hid
  * per lane, 1..2), "attn_splits" (flash-decode splits, 1..128), "skinny_splits"
  * (skinny GEMM K splits, 1..8), "gemm_splits" (ring GEMM: 1 = whole tiles
  * only, 2..16 = stream-K with about that many workgroups per tile),
- * "qkv_reduce" (1 = batched decode steps reduce the qkv split partials in
- * their own launch, not in the attention prologue).  Initial values come
+ * "split_reduce" (1 = batched decode steps reduce the split-K partials of
+ * the qkv, o and down projections in their own launches, not in the
+ * attention prologue / row norm that consume them).  Initial values come
  * from R4Q_GEMV_LPR, R4Q_GEMV_WGS, R4Q_GEMV_UB, R4Q_ATTN_SPLITS,
- * R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, R4Q_QKV_REDUCE, read once.  Results do
+ * R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, R4Q_SPLIT_REDUCE, read once.  Results do
  * not depend on these choices beyond fp32 summation order (split counts) --
  * they exist for sweeps and tests.  Captured decode graphs are keyed by the
  * values in force. */

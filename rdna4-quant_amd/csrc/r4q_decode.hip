@@ -211,13 +211,39 @@ struct Prof {
 // Enqueues one decode step for B rows.  pos_dev/seq_dev: device-held
 // position and length (graph replay), else pos_host.  Input hidden states
 // must already be in bf.h.
-// Batched steps (B > 1): the qkv projection's K split partials are summed by
-// the attention prologue when the skinny GEMM splits K into 2..kMaxQkvSplits.
-bool qkv_partials_in_attention(int64_t B, const Dims& dm, int bits, size_t ws_bytes) {
-  if (B == 1 || tuning().qkv_reduce.load() != 0 || !gemm_skinny_ok(B, dm.qkvN, dm.D, bits))
-    return false;
-  const int S = skinny_splits(B, dm.qkvN, dm.D, bits, ws_bytes);
-  return S >= 2 && S <= kMaxQkvSplits;
+// Batched steps (B > 1): the K-split partials of a skinny projection are
+// summed by the kernel consuming them -- the attention prologue (qkv), the
+// residual + row norm (o, down) -- when the skinny GEMM splits K into 2..
+// that kernel's maximum.  Returns the split count S, or 0 (own reduce).
+enum Consumer { kToAttention, kToRowNorm };
+int consumer_split(int64_t B, int64_t N, int64_t K, int bits, size_t ws_bytes, Consumer c) {
+  if (B == 1 || tuning().split_reduce.load() != 0 || !gemm_skinny_ok(B, N, K, bits)) return 0;
+  const int S = skinny_splits(B, N, K, bits, ws_bytes);
+  if (S < 2) return 0;
+  if (c == kToAttention) return S <= kMaxQkvSplits ? S : 0;
+  return rownorm_psum_ok(N, S) ? S : 0;
+}
+
+// a projection whose partials its consumer sums: launches the GEMM without
+// its reduce and returns S (0: the ordinary launch, y written)
+int project(const void* x, const void* w, const void* s, void* y, int64_t B, int64_t N,
+            int64_t K, int bits, hipStream_t st, const Bufs& bf, Consumer c, int* S) {
+  *S = consumer_split(B, N, K, bits, bf.ws_bytes, c);
+  if (*S == 0) return linear(x, w, s, y, B, N, K, bits, st, bf);
+  int got = 0;
+  R4Q_TRY(gemm_skinny_part_launch(x, w, s, y, B, N, K, bits, st, bf.ws, bf.ws_bytes, &got));
+  R4Q_REQUIRE(got == *S, "skinny GEMM split count changed (%d, expected %d)", got, *S);
+  return R4Q_OK;
+}
+
+// residual + RMSNorm + FWHT-32 of row input a (or of the S split partials of
+// the projection that produced it)
+int rownorm3(const void* a, int S, const void* b, const void* w, void* y, void* res_out,
+             int64_t B, int64_t D, float eps, hipStream_t st, const Bufs& bf) {
+  if (S >= 2)
+    return launch_rownorm_psum(static_cast<const float*>(bf.ws), B * D, S, b, w, y, res_out, B,
+                               D, eps, st);
+  return launch_rownorm(3, a, b, w, y, res_out, B, D, eps, st);
 }
 
 int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host,
@@ -240,11 +266,9 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     // batches: a split-K skinny qkv projection leaves its fp32 partials for
     // the attention prologue to sum (no reduce launch)
     int qkv_nsum = 0;
-    if (!fused && qkv_partials_in_attention(B, dm, y.qkv_bits, bf.ws_bytes)) {
-      R4Q_TRY(gemm_skinny_part_launch(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D,
-                                      y.qkv_bits, st, bf.ws, bf.ws_bytes, &qkv_nsum));
-    } else if (!fused) {
-      R4Q_TRY(linear(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st, bf));
+    if (!fused) {
+      R4Q_TRY(project(bf.rot, y.qkv_w, y.qkv_s, bf.qkv, B, dm.qkvN, D, y.qkv_bits, st, bf,
+                      kToAttention, &qkv_nsum));
     } else if (li == 0) {  // input hidden state: plain RMSNorm
       R4Q_TRY(gemv_norm_launch(bf.h, nullptr, y.in_norm, nullptr, eps, y.qkv_w, y.qkv_s, bf.qkv,
                                dm.qkvN, D, y.qkv_bits, st));
@@ -265,7 +289,9 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
                                 bf.rot, dm.qd, B, dm.H, dm.Hk, dm.max_seq, pos_host + 1, seq_dev,
                                 nsplit, 1, bf.attn, st, &qk));
     prof.mark(st, kGemv);
-    R4Q_TRY(linear(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st, bf));
+    int o_nsum = 0;  // batches: o's split partials summed by the row norm below
+    R4Q_TRY(project(bf.rot, y.o_w, y.o_s, bf.o, B, D, dm.qd, y.o_bits, st, bf, kToRowNorm,
+                    &o_nsum));
     // gate/up: r = fp16(o + h), RMSNorm + FWHT in the staging and, for
     // INT4/INT8, the SiLU-gate in the epilogue: fp16 FWHT'd output for the
     // whole 64-row units below the split (a multiple of the CU count, one
@@ -273,6 +299,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
     // 1); the down GEMV applies the FWHT-32 to that part in its staging.
     // (A unit map alone has 544 units for 256 CUs at I = 17408.)
     const bool silu_fused = fused && y.gu_bits != 16 && gemv_silu_ok(2 * I, D, y.gu_bits);
+    int d_nsum = 0;  // batches: down's split partials summed by the next row norm
     if (silu_fused) {
       // (40-layer step, ctx 2048: 2.925 ms; every element as fp32 pairs:
       // 2.99 ms; every element in units: 3.02 ms)
@@ -289,7 +316,7 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
                                  2 * I, D, y.gu_bits, st));
       } else {
         prof.mark(st, kNorm);
-        R4Q_TRY(launch_rownorm(3, bf.o, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st));
+        R4Q_TRY(rownorm3(bf.o, o_nsum, bf.h, y.post_norm, bf.rot, bf.r, B, D, eps, st, bf));
         prof.mark(st, kGemv);
         if (gemm_skinny_silu_ok(B, I, D, y.gu_bits, bf.ws_bytes)) {
           // split-K skinny GEMM whose reduce applies the SiLU gate + FWHT-32
@@ -305,13 +332,14 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
         R4Q_TRY(launch_silu(true, bf.gu, bf.gu + I, bf.y, B, I, 2 * I, I, st));
       }
       prof.mark(st, kGemv);
-      R4Q_TRY(linear(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st, bf));
+      R4Q_TRY(project(bf.y, y.down_w, y.down_s, bf.d, B, D, I, y.down_bits, st, bf, kToRowNorm,
+                      &d_nsum));
     }
     if (!fused) {
       prof.mark(st, kNorm);
       const void* nxt = (li + 1 < dm.L) ? m->layers[li + 1].in_norm : m->final_norm;
-      R4Q_TRY(launch_rownorm(3, bf.d, bf.r, nxt ? nxt : m->layers[0].in_norm, bf.rot, bf.h, B, D,
-                             eps, st));
+      R4Q_TRY(rownorm3(bf.d, d_nsum, bf.r, nxt ? nxt : m->layers[0].in_norm, bf.rot, bf.h, B, D,
+                       eps, st, bf));
     }
   }
   // h holds the final residual stream (fp16(d + r)) once this block is done
@@ -496,7 +524,7 @@ std::vector<uint8_t> graph_key(int kind, const r4q_model* m, int64_t B, int nspl
   const Tuning& tu = tuning();
   const int knobs[] = {tu.gemv_lpr.load(),      tu.gemv_wgs.load(),    tu.gemv_ub.load(),
                        tu.attn_splits.load(),   tu.skinny_splits.load(), tu.gemm_splits.load(),
-                       tu.qkv_reduce.load()};
+                       tu.split_reduce.load()};
   std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 16 +
                          sizeof(extra) + sizeof(epoch) + sizeof(SampleCfg) + sizeof(knobs));
   uint8_t* p = k.data();
@@ -581,16 +609,19 @@ extern "C" int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int6
   Dims dm;
   R4Q_TRY(validate(m, B, dm));
   const size_t gws = step_gemm_ws(m, dm, B);
-  int fused = 0, qkv_sum = 0;
+  int fused = 0, folded = 0;
   for (int li = 0; li < dm.L; ++li) {
     const int bits = m->layers[li].gu_bits;
     fused += B == 1 ? (bits != 16 && gemv_silu_ok(2 * (int64_t)dm.I, dm.D, bits))
                     : gemm_skinny_silu_ok(B, dm.I, dm.D, bits, gws);
-    qkv_sum += qkv_partials_in_attention(B, dm, m->layers[li].qkv_bits, gws);
+    const r4q_layer& y = m->layers[li];
+    folded += consumer_split(B, dm.qkvN, dm.D, y.qkv_bits, gws, kToAttention) > 0;
+    folded += consumer_split(B, dm.D, dm.qd, y.o_bits, gws, kToRowNorm) > 0;
+    folded += consumer_split(B, dm.D, dm.I, y.down_bits, gws, kToRowNorm) > 0;
   }
   out[0] = attn_num_splits(m->max_seq, B, dm.Hk);
   out[1] = fused;
-  if (n >= 3) out[2] = qkv_sum;
+  if (n >= 3) out[2] = folded;
   return R4Q_OK;
 }
 

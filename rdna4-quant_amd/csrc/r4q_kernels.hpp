@@ -10,6 +10,12 @@ namespace r4q {
 // mode: 0 rmsnorm, 1 residual+rmsnorm, 2 rmsnorm+FWHT, 3 residual+rmsnorm+FWHT
 int launch_rownorm(int mode, const void* a, const void* b, const void* w, void* y,
                    void* res_out, int64_t rows, int64_t D, float eps, hipStream_t st);
+// Mode 3 with a = fp16(split-order sum of S fp32 planes ap[s * plane + row * D + i])
+// (a split-K projection's partials), equal to its reduce followed by mode 3.
+bool rownorm_psum_ok(int64_t D, int S);
+int launch_rownorm_psum(const float* ap, int64_t plane, int S, const void* b, const void* w,
+                        void* y, void* res_out, int64_t rows, int64_t D, float eps,
+                        hipStream_t st);
 int launch_silu(bool fwht, const void* g, const void* u, void* y, int64_t rows, int64_t I,
                 int64_t in_stride, int64_t out_stride, hipStream_t st);
 int check_head_norm_rope_kv(const void* qkv, const void* qw, const void* kw, const void* q_out,

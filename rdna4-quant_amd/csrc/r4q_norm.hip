@@ -61,6 +61,78 @@ __global__ __launch_bounds__(1024) void rownorm_kernel(const uint16_t* __restric
   }
 }
 
+// rownorm_kernel<3> (residual + RMSNorm + FWHT-32) whose input a is the
+// split-K sum of a projection, a = fp16(sum over s < S of ap[s * plane +
+// row * D + i]) in split order -- the arithmetic of gemm_skinny_reduce_kernel
+// -- so the outputs equal that reduce followed by rownorm_kernel<3>.  The S
+// planes are read coalesced by the whole workgroup while the thread's
+// residual and weight chunks are in flight, and the fp16 row is staged in
+// LDS; then one thread per 32-chunk as in rownorm_kernel (the threads past
+// the chunks add exact zeros to the sum of squares).  KF float4 per thread
+// per plane: D <= 4 * KF * kPsumThreads.
+constexpr int kPsumThreads = 512;
+constexpr int kPsumMaxS = 4;
+template <int KF>
+__global__ __launch_bounds__(kPsumThreads) void rownorm_psum_kernel(
+    const float* __restrict__ ap, int64_t plane, int S, const uint16_t* __restrict__ b,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ y, uint16_t* __restrict__ res_out,
+    int D, float eps) {
+  __shared__ float red[16];
+  __shared__ __align__(16) uint32_t as[2 * KF * kPsumThreads];  // the fp16 row
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, nch = D / 32, nf = D / 4;
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  f4v v[KF][kPsumMaxS];
+  const float* pr = ap + row * D;
+#pragma unroll
+  for (int k = 0; k < KF; ++k) {
+    const int f = min(t + k * kPsumThreads, nf - 1);  // clamped, unused past nf
+#pragma unroll
+    for (int z = 0; z < kPsumMaxS; ++z)
+      v[k][z] = *reinterpret_cast<const f4v*>(pr + min(z, S - 1) * plane + 4 * f);
+  }
+  uint32_t bv[16], g[16];
+  const int c = min(t, nch - 1);
+  load16w(b + row * D + c * 32, bv);
+  load16w(w + c * 32, g);
+#pragma unroll
+  for (int k = 0; k < KF; ++k) {
+    const int f = t + k * kPsumThreads;
+    if (f < nf) {
+      f4v a = v[k][0];
+#pragma unroll
+      for (int z = 1; z < kPsumMaxS; ++z)
+        if (z < S) a += v[k][z];
+      as[2 * f] = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
+      as[2 * f + 1] = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
+    }
+  }
+  __syncthreads();
+  uint32_t r[16];
+  float ss = 0.f;
+  if (t < nch) {
+    uint32_t av[16];
+    const u4_t* s4 = reinterpret_cast<const u4_t*>(as + 16 * t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u4_t d = s4[i];
+      av[4 * i] = d[0];
+      av[4 * i + 1] = d[1];
+      av[4 * i + 2] = d[2];
+      av[4 * i + 3] = d[3];
+    }
+    ss = norm_chunk_sumsq<true>(av, bv, r, ss);
+  }
+  const float tot = block_sum(ss, red);
+  const float rrms = 1.0f / __builtin_sqrtf(tot / (float)D + eps);
+  if (t < nch) {
+    uint32_t o[16];
+    store16w(res_out + row * D + t * 32, r);
+    norm_chunk_scale<true>(r, g, rrms, o);
+    store16w(y + row * D + t * 32, o);
+  }
+}
+
 __global__ __launch_bounds__(256) void fwht32_kernel(const uint16_t* __restrict__ x,
                                                      uint16_t* __restrict__ y, int64_t nch) {
   const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -212,6 +284,35 @@ int launch_rownorm(int mode, const void* a, const void* b, const void* w, void* 
     case 2: return rownorm<2>(a, b, w, y, res_out, rows, D, eps, st, "rmsnorm_fwht");
     default: return rownorm<3>(a, b, w, y, res_out, rows, D, eps, st, "res_rmsnorm_fwht");
   }
+}
+
+bool rownorm_psum_ok(int64_t D, int S) {
+  return D % 32 == 0 && D > 0 && D <= 4 * 4 * kPsumThreads && S >= 2 && S <= kPsumMaxS;
+}
+
+int launch_rownorm_psum(const float* ap, int64_t plane, int S, const void* b, const void* w,
+                        void* y, void* res_out, int64_t rows, int64_t D, float eps,
+                        hipStream_t st) {
+  R4Q_REQUIRE(ap && b && w && y && res_out && rows >= 0, "res_rmsnorm_fwht (split sum): null pointer");
+  R4Q_REQUIRE(rownorm_psum_ok(D, S), "res_rmsnorm_fwht (split sum): D=%lld S=%d unsupported",
+              (long long)D, S);
+  R4Q_REQUIRE(plane >= rows * D && al16(ap) && al16(b) && al16(w) && al16(y) && al16(res_out),
+              "res_rmsnorm_fwht (split sum): bad plane or alignment");
+  if (rows == 0) return R4Q_OK;
+  const int kf = (int)((D / 4 + kPsumThreads - 1) / kPsumThreads);
+#define R4Q_PSUM(KF)                                                                            \
+  hipLaunchKernelGGL((rownorm_psum_kernel<KF>), dim3((unsigned)rows), dim3(kPsumThreads), 0, st, \
+                     ap, plane, S, static_cast<const uint16_t*>(b),                             \
+                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y),                \
+                     static_cast<uint16_t*>(res_out), (int)D, eps)
+  switch (kf) {
+    case 1: R4Q_PSUM(1); break;
+    case 2: R4Q_PSUM(2); break;
+    case 3: R4Q_PSUM(3); break;
+    default: R4Q_PSUM(4);
+  }
+#undef R4Q_PSUM
+  return launch_status("res_rmsnorm_fwht (split sum)");
 }
 
 int launch_silu(bool fwht, const void* g, const void* u, void* y, int64_t rows, int64_t I,

@@ -45,7 +45,7 @@ const Knob kKnobs[] = {
     {"attn_splits", "R4Q_ATTN_SPLITS", &Tuning::attn_splits, 1, 128, false},
     {"skinny_splits", "R4Q_SKINNY_SPLITS", &Tuning::skinny_splits, 1, 8, false},
     {"gemm_splits", "R4Q_GEMM_SPLITS", &Tuning::gemm_splits, 1, 16, false},
-    {"qkv_reduce", "R4Q_QKV_REDUCE", &Tuning::qkv_reduce, 1, 1, false},
+    {"split_reduce", "R4Q_SPLIT_REDUCE", &Tuning::split_reduce, 1, 1, false},
 };
 
 bool knob_ok(const Knob& k, long x) {

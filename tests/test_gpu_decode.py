@@ -78,27 +78,28 @@ def test_qwen3_width_batch8_step_vs_oracle(dev):
         assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
 
 
-def test_qwen3_width_batch8_qkv_partials_summed_in_attention_bit_exact(dev):
-    """Batch 8 at full width: the qkv projection's split-K partials summed in
-    the attention prologue (split order, rounded to fp16) give the same
-    logits and FP8 K/V bytes, bit for bit, as the separate reduce launch
-    (qkv_reduce override), INT4 and INT8 qkv layers."""
+def test_qwen3_width_batch8_split_partials_summed_in_consumers_bit_exact(dev):
+    """Batch 8 at full width: the split-K partials of the qkv, o and down
+    projections summed by the kernels that consume them (attention prologue,
+    residual + row norm; split order, rounded to fp16) give the same logits
+    and FP8 K/V bytes, bit for bit, as separate reduce launches (split_reduce
+    override); INT4 and INT8 layers."""
     import r4q_lib as R
-    bits = {(1, "qkv"): 8}
+    bits = {(1, "qkv"): 8, (0, "o"): 8, (1, "down"): 8}
     m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=4096, max_seq=96, seed=14, bits=bits,
               batch=8, fill=60, kv_scale=True)
-    assert plan(m, 8, 3)[2] == 2, "qkv partials not summed in the attention prologue"
+    assert plan(m, 8, 3)[2] == 6, "split partials not summed by their consumers"
     h = _hidden(m, 15, rows=8).to(dev)
     pos = 60
     runs = []
     for knob in (0, 1):
-        R.tune("qkv_reduce", knob)
+        R.tune("split_reduce", knob)
         try:
-            assert plan(m, 8, 3)[2] == (2 if knob == 0 else 0)
+            assert plan(m, 8, 3)[2] == (6 if knob == 0 else 0)
             lg = step_logits(m, h, pos).clone()
             kv = [gpu_kv_at(m, pos, b) for b in range(8)]
         finally:
-            R.tune("qkv_reduce", 0)
+            R.tune("split_reduce", 0)
         runs.append((lg, kv))
     (la, kva), (lb, kvb) = runs
     assert torch.isfinite(la.float()).all()
