@@ -1260,13 +1260,14 @@ static int64_t host_sk_owner(int64_t u, int64_t TU, int64_t sk) {
 }
 
 RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
-  // Every CU gets the same number of K units: when the tiles do not fill
-  // whole rounds of 256 workgroups, the last one to two rounds' tiles are
-  // shared out by stream-K (at least a whole tile's work per workgroup when
-  // there are more tiles than CUs, so that a tile is cut at most twice).
-  // Whole tiles when their rounds are at least 7/8 full: the partials and
-  // their reduce then cost what the idle CUs would (the LM head of a
-  // 512-token prompt, 1188 tiles in 5 rounds: 1109 us whole, 1116 us shared).
+  // Every CU gets the same number of K units: the tiles of the full rounds
+  // of 256 workgroups are computed whole, the remaining tiles' units are
+  // shared by 256 stream-K workgroups (each then writes at most two fp32
+  // partials: 512 x 34816 x 5120, 272 tiles, INT4 271 -> 238 us against
+  // sharing every tile out).  Whole tiles throughout when their rounds are
+  // at least 7/8 full: the partials and their reduce then cost what the idle
+  // CUs would (the LM head of a 512-token prompt, 1188 tiles in 5 rounds:
+  // 1109 us whole, 1116 us shared).
   const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
   const int KS = wbits == 4 ? Ring<4>::KS : wbits == 8 ? Ring<8>::KS : Ring<16>::KS;
   RingPlan pl;
@@ -1279,8 +1280,10 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
   } else if (v == 1 || 8 * tiles >= 7 * kRingCUs * ((tiles + kRingCUs - 1) / kRingCUs)) {
     dp = tiles;
   } else if (tiles > kRingCUs) {
-    dp = (tiles / kRingCUs - 1) * kRingCUs;
-    sk = kRingCUs;
+    dp = (tiles / kRingCUs) * kRingCUs;
+    // no more stream-K workgroups than shared units: every one owns at
+    // least one, so every partial slot the reduce reads is written
+    sk = std::min<int64_t>(kRingCUs, (tiles - dp) * pl.U);
   } else {
     dp = 0;
     sk = std::min<int64_t>(kRingCUs, tiles * pl.U);
