@@ -750,10 +750,15 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   // most one per CU (measured 9.1 -> 8.2 us for 7168 x 5120 INT4), except
   // in the SiLU maps: the unit map needs one workgroup per 64-row unit (as
   // does the split map when it has units); pair steps alone measured best
-  // at 768.
+  // at 768.  Two exceptions, measured on MI355X (cold weights, graph-replayed):
+  // a plain GEMV of at most 3 x 256 steps runs one workgroup per CU (5120 x
+  // 5120 INT4: 214 workgroups of 3 steps 4.74 us, 640 of 1: 5.22 us, 320 of
+  // 2: 5.65 us), and a fused-norm GEMV at 64 lanes per row two per CU (7168 x
+  // 5120 INT8: 448 workgroups of 4 steps 9.59 us, 256 of 7: 10.5 us).
   const bool nrm = xm == kXNorm;
-  const int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : 256)
-                       : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
+  int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : lpr == 64 ? 512 : 256)
+                 : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
+  if (xm == kXPlain && epi == kEpiRows && (nsteps + 255) / 256 <= 3) dflt = 256;
   const int wgs_o = tuning().gemv_wgs.load(), ub_o = tuning().gemv_ub.load();
   const int max_wg = wgs_o ? wgs_o : dflt;
   const int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
