@@ -1067,46 +1067,75 @@ __global__ __launch_bounds__(256) void gemm_skinny_reduce_kernel(const float* __
 }
 
 // Split sum fused with the SiLU gate of a gate/up projection (N = 2I
-// columns: gate 0..I-1, up I..2I-1).  Thread c of row m sums the 32 gate and
-// 32 up columns of chunk c over the splits in order and rounds each sum to
-// fp16 (what gemm_skinny_reduce_kernel stores), then stores
-// FWHT-32(silu(g) * u) in fp16 as silu_kernel<true> does.  64-thread
-// workgroups: a row holds only I / 32 chunks.
-__device__ __forceinline__ void skinny_sum32(const float* __restrict__ p, int64_t plane, int S,
-                                             float* v) {
+// columns: gate 0..I-1, up I..2I-1), four lanes per 32-column chunk: lane q
+// of chunk c of row m sums gate and up columns 32c + 8q .. + 7 over the
+// splits in order and rounds each sum to fp16 (what gemm_skinny_reduce_kernel
+// stores), applies silu(g) * u as silu_kernel<true> does, then runs the
+// butterfly stages 1, 2, 4 of the FWHT-32 in registers and stages 8 and 16
+// with the lanes q ^ 1 and q ^ 2 -- the stage order and (a + b, a - b) pairs
+// of fwht32, so the fp16 output is the same bit for bit.  (One thread per
+// chunk left 72 waves on the chip for I = 17408 and took 6.2 us.)
+__device__ __forceinline__ void skinny_sum8(const float* __restrict__ p, int64_t plane, int S,
+                                            float* v) {
   const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 t = q[i];
-    v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
-  }
+  float4 t0 = q[0], t1 = q[1];
+  v[0] = t0.x, v[1] = t0.y, v[2] = t0.z, v[3] = t0.w;
+  v[4] = t1.x, v[5] = t1.y, v[6] = t1.z, v[7] = t1.w;
   for (int z = 1; z < S; ++z) {
     q = reinterpret_cast<const float4*>(p + z * plane);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 t = q[i];
-      v[4 * i] += t.x, v[4 * i + 1] += t.y, v[4 * i + 2] += t.z, v[4 * i + 3] += t.w;
-    }
+    t0 = q[0];
+    t1 = q[1];
+    v[0] += t0.x, v[1] += t0.y, v[2] += t0.z, v[3] += t0.w;
+    v[4] += t1.x, v[5] += t1.y, v[6] += t1.z, v[7] += t1.w;
   }
 }
 
-__global__ __launch_bounds__(64) void gemm_skinny_reduce_silu_kernel(
+constexpr int kSiluRedThreads = 256;
+__global__ __launch_bounds__(kSiluRedThreads) void gemm_skinny_reduce_silu_kernel(
     const float* __restrict__ part, uint16_t* __restrict__ Y, int M, int I, int S) {
 #pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
-  const int c = blockIdx.x * 64 + threadIdx.x, m = blockIdx.y;
-  if (c * 32 >= I) return;
+  const int tid = blockIdx.x * kSiluRedThreads + threadIdx.x, m = blockIdx.y;
+  const int c = tid >> 2, q = tid & 3;
+  // lanes past the row read chunk 0 and store nothing, but take part in the
+  // cross-lane stages of their chunk group
+  const bool live = c * 32 < I;
   const int64_t plane = (int64_t)M * 2 * I;
-  const float* pg = part + (int64_t)m * 2 * I + c * 32;
-  float a[32], b[32];
-  skinny_sum32(pg, plane, S, a);
-  skinny_sum32(pg + I, plane, S, b);
+  const float* pg = part + (int64_t)m * 2 * I + (live ? c : 0) * 32 + 8 * q;
+  float a[8], b[8];
+  skinny_sum8(pg, plane, S, a);
+  skinny_sum8(pg + I, plane, S, b);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
+  for (int i = 0; i < 8; ++i) {
     const float g = h2f(f2h(a[i])), u = h2f(f2h(b[i]));
     a[i] = g / (1.0f + expf(-g)) * u;
   }
-  fwht32(a);
-  store32h(Y + (int64_t)m * I + c * 32, a);
+#pragma unroll
+  for (int step = 1; step < 8; step <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2 * step) {
+#pragma unroll
+      for (int j = i; j < i + step; ++j) {
+        const float x = a[j], y = a[j + step];
+        a[j] = x + y;
+        a[j + step] = x - y;
+      }
+    }
+  }
+#pragma unroll
+  for (int lm = 1; lm <= 2; lm <<= 1) {  // stages 8 and 16: partner lane q ^ lm
+    const bool upper = (q & lm) != 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float o = __shfl_xor(a[j], lm);
+      a[j] = upper ? o - a[j] : a[j] + o;
+    }
+  }
+  if (!live) return;
+  u4_t w;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = (uint32_t)f2h(a[2 * k] * kInvSqrt32) | ((uint32_t)f2h(a[2 * k + 1] * kInvSqrt32) << 16);
+  *reinterpret_cast<u4_t*>(Y + (int64_t)m * I + c * 32 + 8 * q) = w;
 }
 
 }  // namespace
@@ -1195,8 +1224,9 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   if (keep_part) return R4Q_OK;
   if (silu_I > 0) {
     hipLaunchKernelGGL(gemm_skinny_reduce_silu_kernel,
-                       dim3((unsigned)((silu_I / 32 + 63) / 64), (unsigned)M), dim3(64), 0, st,
-                       part, yp, (int)M, (int)silu_I, S);
+                       dim3((unsigned)((silu_I / 8 + kSiluRedThreads - 1) / kSiluRedThreads),
+                            (unsigned)M),
+                       dim3(kSiluRedThreads), 0, st, part, yp, (int)M, (int)silu_I, S);
     R4Q_TRY(launch_status("gemm_skinny_reduce_silu"));
   } else if (S > 1) {
     hipLaunchKernelGGL(gemm_skinny_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M),
