@@ -8,13 +8,14 @@
 // weight byte is read from HBM once per M-tile and never written back.
 //
 // Three kernels, by shape:
-//  * gemm_ring_kernel (M >= 256, INT4 / INT8): 256 x 256 tiles, X and the
-//    raw weights copied global -> LDS through a ring, the weights
-//    dequantised per wave in registers, the K units of the tiles shared
-//    evenly by the CUs (stream-K, deterministic reduce over a caller
-//    workspace; see its comment);
-//  * gemm_mfma_kernel (17 <= M < 256, and FP16 weights): 128 x 128 tiles,
-//    X and the dequantised W staged in LDS per 32-wide K step;
+//  * gemm_ring_kernel (M >= 256, INT4 / INT8 / FP16): 256 x 256 tiles, X
+//    and the raw weights copied global -> LDS through a ring, the weights
+//    dequantised per wave in registers (FP16: read as they are), the K
+//    units of the tiles beyond the full rounds of 256 shared evenly by the
+//    CUs (stream-K, deterministic reduce over a caller workspace; see its
+//    comment);
+//  * gemm_mfma_kernel (17 <= M < 256): 128 x 128 tiles, X and the
+//    dequantised W staged in LDS per 32-wide K step;
 //  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows
 //    through an LDS ring (split along K for narrow N).
 // Dequantised values equal r4q_dequant_int4/8 bit-for-bit
@@ -233,7 +234,7 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 }
 
 // ---------------------------------------------------------------------
-// Prefill GEMM for M >= 256 with INT4 / INT8 weights: a workgroup of 4 waves
+// Prefill GEMM for M >= 256 with INT4 / INT8 / FP16 weights: a workgroup of 4 waves
 // (one per SIMD) owns a 256 x 256 output tile, each wave 256 rows x 64
 // columns (16 x 4 MFMA tiles, 256 fp32 accumulators per lane, in AGPRs).
 // The K loop of the 128 x 128 kernel above is bound by global-load latency
@@ -250,8 +251,11 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 // LDS into registers (one 4-byte INT4 / 8-byte INT8 read per fragment
 // instead of 16 bytes of fp16), one step ahead, interleaved with the MFMAs
 // of the current step; the fp16 values equal r4q_dequant_int4/8 bit for bit.
-// X fragments 0-3 of a step are read during the previous step's MFMAs, so
-// that each step starts its MFMAs without waiting for LDS.
+// FP16 weights have no super-steps: each X stage also holds the step's 64
+// bytes of the 256 weight rows, laid out like X, and the B fragments are
+// read from it like X fragments.
+// Each X fragment register is refilled with the next step's fragment right
+// after its MFMAs, so that each step starts its MFMAs without waiting for LDS.
 // LDS layouts are bank-conflict-free for their fragment reads (measured on
 // MI355X with a read-throughput probe):
 //  * X rows are 64 bytes per step; the 16-byte piece p of row r sits in slot
