@@ -110,9 +110,11 @@ R4Q_API int r4q_gemv(const void* x, const void* w, const void* sz, void* y,
 R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
              int64_t M, int64_t N, int64_t K, int wbits, void* stream);
 /* Device workspace (bytes, written to *bytes; 0: none) that lets r4q_gemm_ws
- * split K loops over more workgroups: for M >= 256 INT4/INT8 the K units of
- * the output tiles are shared evenly by the CUs (stream-K), for 2 <= M <= 16
- * the weight tiles split along K.  Split tiles keep fp32 partials in the
+ * split K loops over more workgroups: for M >= 256 (INT4 / INT8 / FP16) the
+ * output tiles of the full rounds of 256 workgroups are computed whole and
+ * the K units of the remaining tiles are shared evenly by the CUs
+ * (stream-K; none when the tiles fill their rounds to 7/8 or more), for
+ * 2 <= M <= 16 the weight tiles split along K.  Split tiles keep fp32 partials in the
  * workspace, summed in a fixed order (deterministic for a given shape and
  * workspace size; within fp32 rounding of the unsplit product).  Same role
  * as the rocBLAS workspace behind the reference's at::mm_out in
