@@ -755,13 +755,29 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   // 5120 INT4: 214 workgroups of 3 steps 4.74 us, 640 of 1: 5.22 us, 320 of
   // 2: 5.65 us), and a fused-norm GEMV at 64 lanes per row two per CU (7168 x
   // 5120 INT8: 448 workgroups of 4 steps 9.59 us, 256 of 7: 10.5 us).
+  // Plain GEMVs at <= 32 lanes per row follow the most loaded CU's work,
+  // ceil(workgroups / 256) x (steps per workgroup + 1, for the workgroup's
+  // activation staging and tail): that count is minimised (at most 12 steps
+  // each), with the fewest workgroups among equal counts (17408 x 5120 INT4:
+  // 242 workgroups of 9 steps 9.95 us, 726 of 3: 10.46, 272 of 8: 12.60;
+  // 34816 x 5120: 484 of 9 18.1 us, 871 of 5: 19.4, 544 of 8: 21.4).
   const bool nrm = xm == kXNorm;
   int dflt = nrm ? (lpr == 128 ? 512 : epi != kEpiRows ? 768 : lpr == 64 ? 512 : 256)
                  : (lpr <= 64 ? 1024 : lpr == 128 ? 512 : 768);
   if (xm == kXPlain && epi == kEpiRows && (nsteps + 255) / 256 <= 3) dflt = 256;
   const int wgs_o = tuning().gemv_wgs.load(), ub_o = tuning().gemv_ub.load();
   const int max_wg = wgs_o ? wgs_o : dflt;
-  const int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
+  int64_t per = F > 0 ? 1 : (nsteps + max_wg - 1) / max_wg;
+  if (!wgs_o && xm == kXPlain && epi == kEpiRows && lpr <= 32) {
+    int64_t best = INT64_MAX;
+    for (int64_t p = 1; p <= 12; ++p) {
+      const int64_t cost = ((nsteps + p - 1) / p + 255) / 256 * (p + 1);
+      if (cost <= best) {
+        best = cost;
+        per = p;
+      }
+    }
+  }
   const int64_t grid = (nsteps + per - 1) / per;
   // steps in flight per lane: at most the steps a workgroup has (a deeper
   // ring would re-read its last step)
