@@ -113,8 +113,9 @@ R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
  * split K loops over more workgroups: for M >= 256 (INT4 / INT8 / FP16) the
  * output tiles of the full rounds of 256 workgroups are computed whole and
  * the K units of the remaining tiles are shared evenly by the CUs
- * (stream-K; none when the tiles fill their rounds to 7/8 or more), for
- * 2 <= M <= 16 the weight tiles split along K.  Split tiles keep fp32 partials in the
+ * (stream-K; none when the tiles fill their rounds to 7/8 or more; with at
+ * most 128 tiles each tile is split into floor(256 / tiles) equal pieces),
+ * for 2 <= M <= 16 the weight tiles split along K.  Split tiles keep fp32 partials in the
  * workspace, summed in a fixed order (deterministic for a given shape and
  * workspace size; within fp32 rounding of the unsplit product).  Same role
  * as the rocBLAS workspace behind the reference's at::mm_out in

@@ -12,8 +12,8 @@
 //    and the raw weights copied global -> LDS through a ring, the weights
 //    dequantised per wave in registers (FP16: read as they are), the K
 //    units of the tiles beyond the full rounds of 256 shared evenly by the
-//    CUs (stream-K, deterministic reduce over a caller workspace; see its
-//    comment);
+//    CUs (stream-K) or, with at most 128 tiles, each tile split into equal
+//    pieces (deterministic reduce over a caller workspace; see its comment);
 //  * gemm_mfma_kernel (17 <= M < 256): 128 x 128 tiles, X and the
 //    dequantised W staged in LDS per 32-wide K step;
 //  * gemm_skinny_kernel (2 <= M <= 16): weights streamed once for all rows
@@ -1318,6 +1318,12 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
     // no more stream-K workgroups than shared units: every one owns at
     // least one, so every partial slot the reduce reads is written
     sk = std::min<int64_t>(kRingCUs, (tiles - dp) * pl.U);
+  } else if (kRingCUs / tiles >= 2) {
+    // at most 128 tiles: each split into floor(256 / tiles) equal pieces, so
+    // that every workgroup stays inside one tile and writes one partial
+    // (M = 512: 7168 x 5120 INT4 81.6 -> 67.7 us, 5120 x 17408 125.6 -> 119.7)
+    dp = 0;
+    sk = std::min<int64_t>(tiles * (kRingCUs / tiles), tiles * pl.U);
   } else {
     dp = 0;
     sk = std::min<int64_t>(kRingCUs, tiles * pl.U);
