@@ -298,6 +298,74 @@ def flash_decode_leg(dev, ctx, iters=100):
     return us, Hk * ctx * 2 * D
 
 
+def layer_leg(dev, ctx=2048, reps=5, calls=20, n_layers=3):
+    """Config 1: one Qwen3-14B-shaped decoder layer at batch 1 -- qkv / o /
+    gate_up INT4, down_proj INT8 -- timed as a decode step at position ctx
+    of `n_layers` such layers (fused residual + RMSNorm staging, SiLU-gate
+    epilogue, flash-decode over an FP8 cache of ctx positions, FWHT-32
+    staging of the down projection; 3 layers = 570 MB, more than the 256 MB
+    last-level cache holds, so the weights stream from HBM as in the full
+    step).  `calls` eager steps are captured in one torch hipGraph and
+    replayed `reps` times between HIP events: returns the average
+    microseconds per layer (the step's closing row norm and hidden-state
+    copies included, spread over the layers) and the bytes one layer reads
+    (weights + 4 B/block metadata + KV)."""
+    import torch
+
+    import int4_hip
+    import r4q_synth as S
+    c = S.QWEN3_14B
+    D, I, H, Hk, hd = c["hidden"], c["inter"], c["heads"], c["kv_heads"], c["head_dim"]
+    g = S.gen(11, dev)
+    bits = {"qkv": 4, "o": 4, "gu": 4, "down": 8}
+    lys = [S.make_layer(D, I, H, Hk, hd, g, device=dev, bits=bits) for _ in range(n_layers)]
+    cap = ctx + 1
+    kcs, vcs = [], []
+    for _ in range(n_layers):
+        kc = torch.zeros(1, Hk, cap, hd, dtype=torch.uint8, device=dev)
+        vc = torch.zeros_like(kc)
+        kc[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev))
+        vc[:, :, :ctx] = int4_hip.fp16_to_fp8(S.random_kv_values(Hk, ctx, hd, g, dev))
+        kcs.append(kc)
+        vcs.append(vc)
+    cos, sin = S.rope_tables(hd, cap, c["rope_theta"], dev)
+    had = torch.zeros(32, 32, dtype=torch.float16, device=dev)
+    h = (torch.randn(1, 1, D, generator=torch.Generator().manual_seed(2)) * 0.5).half().to(dev)
+    lists = [[ly[k] for ly in lys]
+             for k in ("qkv_w", "qkv_s", "qkv_N", "o_w", "o_s", "o_N", "gu_w", "gu_s", "gu_N",
+                       "down_w", "down_s", "down_N", "in_norm", "post_norm", "q_norm", "k_norm")]
+    args = lists + [cos, sin, ctx, H, Hk, hd, D, I, c["eps"], kcs, vcs, had]
+    ly = lys[0]
+
+    def step():
+        return int4_hip.decode_step(h, *args, use_graph=False)
+
+    step()  # allocates the context's buffers outside the capture
+    torch.cuda.synchronize()
+    st = torch.cuda.Stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        for _ in range(calls):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    with torch.cuda.stream(st):
+        for _ in range(reps):
+            graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * calls * n_layers)
+    nbytes = 0
+    for n, K in (("qkv", D), ("o", H * hd), ("gu", D), ("down", I)):
+        N, b = ly[n + "_N"], ly[n + "_bits"]
+        nbytes += N * K * b // 8 + N * (K // 32) * 4
+    nbytes += 2 * Hk * hd * ctx
+    del graph, lys, kcs, vcs
+    return us, nbytes
+
+
 def copy_calibration(dev, mib=256, iters=20):
     """A plain copy of known size (fp16 negation: `mib` MiB read, `mib` MiB
     written per launch) whose FETCH_SIZE / WRITE_SIZE counters calibrate the
@@ -548,6 +616,14 @@ def main():
             f"reference strategy (dequantise + vendor fp16 GEMM): {rs['dequant_us']:.1f} + "
             f"{rs['vendor_gemm_us']:.1f} = {rs['us']:.1f} us")
     torch.cuda.empty_cache()
+    layer = None
+    if not args.decode_only:
+        l_us, l_bytes = layer_leg(dev, args.ctx)
+        layer = {"us": round(l_us, 3), "bytes": l_bytes, "gbps": round(l_bytes / l_us / 1e3, 1),
+                 "frac": round(l_bytes / l_us / 1e3 / HBM_PEAK_GBPS, 4)}
+        log(f"one decoder layer (qkv / o / gate_up INT4, down INT8, ctx={args.ctx}): "
+            f"{l_us:.1f} us, {l_bytes / l_us / 1e3:.0f} GB/s")
+        torch.cuda.empty_cache()
 
     log("building synthetic model")
     t0 = time.time()
@@ -658,6 +734,8 @@ def main():
             "read_floor_us": round(rf_us, 3),
             "frac_of_read_floor": round(rf_us / us, 4),
         },
+        # config 1: one decoder layer's GEMVs + fusions (+ its attention) at batch 1
+        "layer": layer,
         # config 2: flash-decode alone, batch 1, cold KV (ring > 512 MB), per ctx
         "flash_decode": attn,
         # config 3: prefill GEMM, M = 512, INT4, K x N, fraction of 2.5 PF fp16 MFMA
