@@ -128,11 +128,14 @@ R4Q_API int r4q_gemm_ws(const void* x, const void* w, const void* sz, void* y,
                         size_t ws_bytes, void* stream);
 /* Batched gate/up projection with the SiLU gate: y[M,I] fp16 =
  * FWHT-32(silu(g) * u), [g; u] = x W^T over W's 2I rows [gate; up],
- * bit-identical to r4q_gemm_ws into [M, 2I] followed by r4q_silu_mul_fwht
- * (in/out strides 2I / I).  The split-K partial sum, the gate and the
- * FWHT run in one kernel.  For 2 <= M <= 16 and I % 32 == 0 with a
- * workspace of r4q_gemm_workspace_bytes(M, 2I, K) that splits K; other
- * shapes are rejected.  Replaces the batched decode step's launch_gemv
+ * bit-identical to r4q_gemm_ws with the same workspace into [M, 2I]
+ * followed by r4q_silu_mul_fwht (in/out strides 2I / I).  For 2 <= M <= 16
+ * and I % 32 == 0.  With a workspace that splits K (r4q_gemm_workspace_bytes
+ * (M, 2I, K)) the split-K partial sum, the gate and the FWHT run in one
+ * reduce kernel; for M <= 8 without one (NULL / too small to split) the
+ * GEMM runs unsplit over tiles of 32 gate rows and the 32 up rows of the
+ * same indices, with the gate and the FWHT in its epilogue.  Other cases
+ * are rejected.  Replaces the batched decode step's launch_gemv
  * (gate_up) + silu_hadamard_ds pair (hip:1031-1051, hip:2508-2516). */
 R4Q_API int r4q_gemm_silu_fwht_ws(const void* x, const void* w, const void* sz, void* y,
                                   int64_t M, int64_t I, int64_t K, int wbits, void* ws,

@@ -858,6 +858,14 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
 // of a row sit in LDS slot piece ^ (row & 7) (bank spread).
 // Split-K (S > 1): the workgroup covers steps [s kps, (s+1) kps) and writes
 // fp32 partials part[s][m][n]; gemm_skinny_reduce_kernel sums them in order.
+// SiLU epilogue (SILU, unsplit, M <= 8; W = [gate; up] over 2I rows): tile t
+// holds gate rows 32t .. 32t+31 (waves 0, 1) and the up rows I + 32t ..
+// of the same indices (waves 2, 3); its fp16-rounded results meet in LDS
+// and each of the 256 threads finishes one (activation row, element):
+// y[m][32t + i] = fp16(FWHT32(silu(g) * u)) with the butterflies across 32
+// lanes -- the arithmetic of silu_kernel<true>.  A weight row's MFMA chain
+// does not depend on the tile it sits in, so the result equals the unsplit
+// GEMM followed by that kernel bit for bit.
 constexpr int kSkTile = 64;   // weight rows per workgroup
 constexpr int kSkStages = 3;  // steps in flight
 constexpr int kSkMaxSplits = 8;
@@ -882,27 +890,29 @@ struct SkRing {
 // Per-lane source offsets of the copies of one ring step (bytes from the
 // step's uniform bases W + 128 kb, SZ + kb * words, X + kb * kKS; rows past N /
 // M clamped to the last one), computed once per workgroup: a step's copies
-// then cost no vector arithmetic.
+// then cost no vector arithmetic.  Tile rows 0..31 are weight rows n0 ..,
+// tile rows 32..63 are n1 .. (n1 = n0 + 32 except in the SiLU map).
 template <int WBITS, int MR>
 struct SkCopy {
   using R = SkRing<WBITS, MR>;
   static constexpr int kWpr = R::kSRow / 4;  // scale words per row per step
   uint32_t wo[2], so[R::kCS > 0 ? R::kCS : 1], xo[R::kCX];
 
-  __device__ __forceinline__ void init(int M, int N, int K, int n0, int wave, int lane) {
+  __device__ __forceinline__ void init(int M, int N, int K, int n0, int n1, int wave, int lane) {
     const uint32_t row_bytes = (uint32_t)K * WBITS / 8;
+    auto row = [&](int r) { return min(r < 32 ? n0 + r : n1 + (r - 32), N - 1); };
 #pragma unroll
     for (int i = 0; i < 2; ++i) {  // weights: copy c covers tile rows 8c .. 8c+7
       const int c = 2 * wave + i, r = 8 * c + (lane >> 3);
       const int piece = (lane & 7) ^ (r & 7);
-      wo[i] = (uint32_t)min(n0 + r, N - 1) * row_bytes + 16 * piece;
+      wo[i] = (uint32_t)row(r) * row_bytes + 16 * piece;
     }
     if constexpr (WBITS != 16) {
       constexpr int rpc = 64 / kWpr;  // rows per 256-byte copy
 #pragma unroll
       for (int i = 0; i < R::kCS; ++i) {
         const int c = R::kCS * wave + i, r = rpc * c + lane / kWpr;
-        so[i] = 4u * ((uint32_t)min(n0 + r, N - 1) * (uint32_t)(K / 32) + lane % kWpr);
+        so[i] = 4u * ((uint32_t)row(r) * (uint32_t)(K / 32) + lane % kWpr);
       }
     }
 #pragma unroll
@@ -1006,18 +1016,20 @@ struct SkLoop {
   }
 };
 
-template <int WBITS, int MR>
+template <int WBITS, int MR, bool SILU>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint32_t* __restrict__ SZ,
                                                           uint16_t* __restrict__ Y,
                                                           float* __restrict__ part, int M, int N,
-                                                          int K, int ntiles, int kps) {
+                                                          int K, int ntiles, int kps, int silu_I) {
+  static_assert(!SILU || MR == 8, "the SiLU epilogue maps 8 rows x 32 elements to 256 threads");
   using R = SkRing<WBITS, MR>;
   __shared__ __align__(16) uint8_t ring[kSkStages * R::kStage];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
-  const int n0 = tile * kSkTile;
+  const int n0 = SILU ? 32 * tile : tile * kSkTile;
+  const int n1 = SILU ? silu_I + 32 * tile : n0 + 32;
   const int kt = K / R::kKS;
   const int col = lane & 15, g = lane >> 4;
   const int wrow = 16 * wave + col;                   // this lane's weight row in the tile
@@ -1031,7 +1043,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   lp.kb0 = sp * kps;
   lp.nk = min(kt - lp.kb0, kps);  // >= 1 (host)
   lp.wave = wave;
-  lp.cp.init(M, N, K, n0, wave, lane);
+  lp.cp.init(M, N, K, n0, n1, wave, lane);
   // weight bytes [32 g, 32 g + 32) of row wrow: pieces 2g, 2g+1
   lp.ob0 = 128 * wrow + 16 * ((2 * g) ^ (wrow & 7));
   lp.ob1 = 128 * wrow + 16 * ((2 * g + 1) ^ (wrow & 7));
@@ -1043,7 +1055,29 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   lp.run();
   const f4_t acc = lp.acc;
   wait_copies<0>();  // no copy into LDS outlives the workgroup
-  // C: lane holds activation rows 4g + r, weight row n0 + 16 wave + col
+  // C: lane holds activation rows 4g + r (rows >= MR repeat rows < MR), tile
+  // row 16 wave + col
+  if constexpr (SILU) {
+#pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
+    __syncthreads();  // every wave is done with the ring, which now holds
+    float* us = reinterpret_cast<float*>(ring);  // us[m][tile row], 8 x 64
+    if (g < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) us[(4 * g + r) * 64 + 16 * wave + col] = h2f(f2h(acc[r]));
+    }
+    __syncthreads();
+    const int m = threadIdx.x >> 5, i = threadIdx.x & 31;
+    const float gv = us[m * 64 + i], uv = us[m * 64 + 32 + i];
+    float v = gv / (1.0f + expf(-gv)) * uv;
+#pragma unroll
+    for (int bit = 1; bit <= 16; bit <<= 1) {
+      const float o = __shfl_xor(v, bit);
+      v = (i & bit) ? o - v : v + o;
+    }
+    v *= kInvSqrt32;
+    if (m < M) Y[(int64_t)m * silu_I + 32 * tile + i] = f2h(v);
+    return;
+  }
   const int n = n0 + 16 * wave + col;
   if (n < N) {
 #pragma unroll
@@ -1189,10 +1223,11 @@ size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
 }
 
 namespace {
-// silu_I > 0: N = 2 silu_I gate/up columns, split (S > 1, checked by the
-// caller) and reduced by gemm_skinny_reduce_silu_kernel into y (M x silu_I).
-// silu_I > 0: the reduce applies the SiLU gate; keep_part: no reduce, the S
-// fp32 partial planes stay in ws (S > 1) for the consumer to sum.
+// silu_I > 0: N = 2 silu_I gate/up columns into y (M x silu_I) gated by
+// SiLU + FWHT-32: split (S > 1) and reduced by
+// gemm_skinny_reduce_silu_kernel, or unsplit (S == 1, M <= 8: checked by the
+// caller) with the gate in the GEMM's epilogue.  keep_part: no reduce, the
+// S fp32 partial planes stay in ws (S > 1) for the consumer to sum.
 int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes, int64_t silu_I,
                bool keep_part = false) {
@@ -1206,10 +1241,21 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   const int kps = (int)((kt + S - 1) / S);
   float* part = S > 1 ? static_cast<float*>(ws) : nullptr;
   const dim3 grid((unsigned)(ntiles * S));
-#define R4Q_SKINNY(WB, MRR)                                                                    \
-  hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR>), grid, dim3(256), 0, st, xp, wp, sp, yp,    \
-                     part, (int)M, (int)N, (int)K, (int)ntiles, kps)
   const bool m8 = M <= 8;
+  if (silu_I > 0 && S == 1) {  // unsplit: the SiLU gate in the epilogue (M <= 8, caller)
+#define R4Q_SKINNY_SILU(WB)                                                                      \
+  hipLaunchKernelGGL((gemm_skinny_kernel<WB, 8, true>), dim3((unsigned)(silu_I / 32)), dim3(256), \
+                     0, st, xp, wp, sp, yp, nullptr, (int)M, (int)N, (int)K,                     \
+                     (int)(silu_I / 32), kps, (int)silu_I)
+    if (wbits == 4) R4Q_SKINNY_SILU(4);
+    else if (wbits == 8) R4Q_SKINNY_SILU(8);
+    else R4Q_SKINNY_SILU(16);
+#undef R4Q_SKINNY_SILU
+    return launch_status("gemm_skinny_silu");
+  }
+#define R4Q_SKINNY(WB, MRR)                                                                    \
+  hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR, false>), grid, dim3(256), 0, st, xp, wp, sp, \
+                     yp, part, (int)M, (int)N, (int)K, (int)ntiles, kps, 0)
   switch (wbits) {
     case 4:
       if (m8) R4Q_SKINNY(4, 8);
@@ -1257,14 +1303,14 @@ int gemm_skinny_part_launch(const void* x, const void* w, const void* sz, void* 
 
 bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes) {
   return gemm_skinny_ok(M, 2 * I, K, wbits) && I > 0 && I % 32 == 0 &&
-         skinny_splits(M, 2 * I, K, wbits, ws_bytes) > 1;
+         (M <= 8 || skinny_splits(M, 2 * I, K, wbits, ws_bytes) > 1);
 }
 
 int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                             int64_t I, int64_t K, int wbits, hipStream_t st, void* ws,
                             size_t ws_bytes) {
   R4Q_REQUIRE(gemm_skinny_silu_ok(M, I, K, wbits, ws ? ws_bytes : 0),
-              "gate_up_silu: shape or workspace does not take the split path");
+              "gate_up_silu: needs I %% 32 == 0, and above 8 rows a workspace that splits K");
   return skinny_run(x, w, sz, y, M, 2 * I, K, wbits, st, ws, ws_bytes, I);
 }
 

@@ -71,9 +71,10 @@ int gemm_skinny_part_launch(const void* x, const void* w, const void* sz, void* 
                             int64_t N, int64_t K, int wbits, hipStream_t st, void* ws,
                             size_t ws_bytes, int* S);
 // The same GEMM over N = 2I gate/up columns with the SiLU gate and FWHT-32
-// fused into the split sum: y (M x I fp16) = FWHT-32(silu(gate) * up),
-// equal to the plain GEMM followed by silu_mul_fwht.  Needs the split path
-// (gemm_skinny_silu_ok).
+// fused: y (M x I fp16) = FWHT-32(silu(gate) * up), equal to the plain GEMM
+// with the same workspace followed by silu_mul_fwht.  A workspace that
+// splits K puts the gate in the split sum; without one (M <= 8) it runs in
+// the unsplit GEMM's epilogue (gemm_skinny_silu_ok).
 bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_bytes);
 int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                             int64_t I, int64_t K, int wbits, hipStream_t st, void* ws,

@@ -164,13 +164,18 @@ def test_small_m_path_matches_gemv(dev):
         assert rel_l2(y[r], int4_hip.dbg_gemv(X[r].contiguous(), W, SZ, N, K)) <= 1e-3
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("bits,M,I,K", [(4, 8, 17408, 5120), (8, 8, 17408, 5120), (4, 2, 512, 5120),
                                         (8, 16, 2048, 1024), (16, 4, 1024, 2048)])
-def test_gemm_silu_fwht_matches_gemm_then_silu(dev, bits, M, I, K):
-    """r4q_gemm_silu_fwht_ws (split sum + SiLU gate + FWHT-32 in the reduce)
-    equals r4q_gemm_ws into [M, 2I] followed by r4q_silu_mul_fwht, bit for
-    bit, over two calls that share the workspace."""
+def test_gemm_silu_fwht_matches_gemm_then_silu(dev, bits, M, I, K, split):
+    """r4q_gemm_silu_fwht_ws equals r4q_gemm_ws with the same workspace into
+    [M, 2I] followed by r4q_silu_mul_fwht, bit for bit, over two calls: with
+    a workspace that splits K (split sum + SiLU gate + FWHT-32 in the reduce)
+    and, for M <= 8, without one (the unsplit GEMM over tiles of 32 gate rows
+    and the 32 up rows of the same indices, the gate in its epilogue)."""
     import r4q_lib as R
+    if not split and M > 8:
+        pytest.skip("above 8 rows the gate needs the split path")
     g = S.gen(7 * M + I + K + bits)
     w, sz = S.weight(2 * I, K, bits, g)
     wd = w.to(dev)
@@ -178,37 +183,39 @@ def test_gemm_silu_fwht_matches_gemm_then_silu(dev, bits, M, I, K):
     b = C.c_size_t(0)
     R.call("r4q_gemm_workspace_bytes", M, 2 * I, K, bits, C.byref(b))
     assert b.value > 0
-    ws = torch.empty(b.value, dtype=torch.uint8, device=dev)
+    ws = torch.empty(b.value if split else 0, dtype=torch.uint8, device=dev)
+    wsp = ws.data_ptr() if split else None
     st = R.stream_handle()
     for rep in range(2):
         x = (torch.randn(M, K, generator=g) * (0.5 + rep)).half().to(dev)
         gu = torch.empty(M, 2 * I, dtype=torch.float16, device=dev)
         want = torch.empty(M, I, dtype=torch.float16, device=dev)
         R.call("r4q_gemm_ws", x.data_ptr(), wd.data_ptr(), None if sd is None else sd.data_ptr(),
-               gu.data_ptr(), M, 2 * I, K, bits, ws.data_ptr(), ws.numel(), st)
+               gu.data_ptr(), M, 2 * I, K, bits, wsp, ws.numel(), st)
         R.call("r4q_silu_mul_fwht", gu.data_ptr(), gu.data_ptr() + 2 * I, want.data_ptr(),
                M, I, 2 * I, I, st)
         got = torch.full((M, I), float("nan"), dtype=torch.float16, device=dev)
         R.call("r4q_gemm_silu_fwht_ws", x.data_ptr(), wd.data_ptr(),
                None if sd is None else sd.data_ptr(), got.data_ptr(), M, I, K, bits,
-               ws.data_ptr(), ws.numel(), st)
+               wsp, ws.numel(), st)
         torch.cuda.synchronize()
         assert torch.isfinite(want).all()
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (bits, M, I, K, rep)
 
 
 def test_gemm_silu_fwht_rejects_unsplit_shapes(dev):
-    """One row, I off the 32-chunk grid, or a workspace too small to split K
-    are errors (the caller uses r4q_gemm_ws + r4q_silu_mul_fwht there)."""
+    """One row, I off the 32-chunk grid, or more than 8 rows with a workspace
+    too small to split K are errors (the caller uses r4q_gemm_ws +
+    r4q_silu_mul_fwht there)."""
     import r4q_lib as R
     I, K = 512, 5120
     w, sz = S.weight(2 * I, K, 4, S.gen(5))
     wd, sd = w.to(dev), sz.to(dev)
-    x = torch.zeros(8, K, dtype=torch.float16, device=dev)
-    y = torch.empty(8, I, dtype=torch.float16, device=dev)
+    x = torch.zeros(16, K, dtype=torch.float16, device=dev)
+    y = torch.empty(16, I, dtype=torch.float16, device=dev)
     ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
     st = R.stream_handle()
-    for (M, II, nbytes) in ((1, I, ws.numel()), (8, I - 16, ws.numel()), (8, I, 256)):
+    for (M, II, nbytes) in ((1, I, ws.numel()), (8, I - 16, ws.numel()), (16, I, 256)):
         with pytest.raises(RuntimeError):
             R.call("r4q_gemm_silu_fwht_ws", x.data_ptr(), wd.data_ptr(), sd.data_ptr(),
                    y.data_ptr(), M, II, K, 4, ws.data_ptr(), nbytes, st)
