@@ -349,7 +349,9 @@ R4Q_API int r4q_decode_plan(const r4q_model* m, int64_t B, int32_t* out, int64_t
  * into a hipGraph and replays it with the position held in device memory.
  * Greedy next token (argmax + embedding gather) runs on the device between
  * steps when the model has an embedding; token ids (int64 [num_tokens, B])
- * are written to `tokens_out` when it is not NULL.  B sequences. */
+ * are written to `tokens_out` when it is not NULL.  B sequences.  At most
+ * two steps are queued ahead of the GPU (a deeper queue of steps runs them
+ * slower), so the call returns once all but the last two steps have run. */
 R4Q_API int r4q_decode_bench(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                      int64_t B, int64_t num_tokens, int64_t start_pos,
                      int use_graph, void* tokens_out, void* stream);
