@@ -75,6 +75,36 @@ def bench_args(m, start_pos):
     return S.qwen3_bench_args(m, start_pos)
 
 
+def replay_timed(graph, reps, st, warm=4):
+    """HIP-event time (ms) of `reps` replays of a captured graph on stream
+    `st`, after `warm` untimed replays (in a trace of the config-0 GEMV the
+    first replays after a single warm-up ran 3-5% slower than the later ones),
+    with at most two replays queued ahead of the GPU (the decode loops of the
+    library do the same: a deep queue of replays ran the same work slower).
+    Each replay is enqueued while the one before it still runs, so the GPU
+    does not wait for the host between them."""
+    import torch
+    done = [torch.cuda.Event(), torch.cuda.Event()]
+    with torch.cuda.stream(st):
+        for r in range(warm):
+            if r >= 2:
+                done[r % 2].synchronize()
+            graph.replay()
+            done[r % 2].record(st)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    with torch.cuda.stream(st):
+        for r in range(reps):
+            if r >= 2:
+                done[r % 2].synchronize()
+            graph.replay()
+            done[r % 2].record(st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
+
+
 def gemv_roofline(dev, iters=200, copies=8, eager_tail=0):
     """Average duration of the config-0 INT4 GEMV and its algorithmic bytes.
 
@@ -108,14 +138,7 @@ def gemv_roofline(dev, iters=200, copies=8, eager_tail=0):
     graph.replay()
     torch.cuda.synchronize()
     reps = 5
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    with torch.cuda.stream(st):
-        for _ in range(reps):
-            graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+    us = replay_timed(graph, reps, st) * 1000.0 / (reps * iters)
     # eager launches for per-dispatch counter collection
     for i in range(eager_tail):
         launch(i)
@@ -152,14 +175,7 @@ def read_floor(dev, iters=200, copies=8):
     graph.replay()
     torch.cuda.synchronize()
     reps = 5
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    with torch.cuda.stream(st):
-        for _ in range(reps):
-            graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / (reps * iters), nbytes
+    return replay_timed(graph, reps, st) * 1000.0 / (reps * iters), nbytes
 
 
 def prefill_gemm_leg(dev, iters=20):
@@ -285,14 +301,7 @@ def flash_decode_leg(dev, ctx, iters=100):
     graph.replay()
     torch.cuda.synchronize()
     reps = 3
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    with torch.cuda.stream(st):
-        for _ in range(reps):
-            graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+    us = replay_timed(graph, reps, st) * 1000.0 / (reps * iters)
     del graph
     R.call("r4q_ctx_destroy", ctx_h)
     return us, Hk * ctx * 2 * D
@@ -349,14 +358,7 @@ def layer_leg(dev, ctx=2048, reps=5, calls=20, n_layers=3):
             step()
     graph.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    with torch.cuda.stream(st):
-        for _ in range(reps):
-            graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (reps * calls * n_layers)
+    us = replay_timed(graph, reps, st) * 1000.0 / (reps * calls * n_layers)
     nbytes = 0
     for n, K in (("qkv", D), ("o", H * hd), ("gu", D), ("down", I)):
         N, b = ly[n + "_N"], ly[n + "_bits"]
