@@ -78,6 +78,26 @@ def test_qwen3_width_batch8_step_vs_oracle(dev):
         assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
 
 
+def test_qwen3_width_batch3_step_vs_oracle(dev):
+    """Batch 3 at full width: gate_up runs unsplit with the SiLU gate in the
+    skinny GEMM's epilogue on 3 of its 8 activation rows (the rest repeat the
+    last row and are not stored), INT4 and INT8; every row against the
+    oracle under KV teacher forcing."""
+    bits = {(1, "gu"): 8, (0, "down"): 8}
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=2048, max_seq=96, seed=21, bits=bits,
+              batch=3, fill=40, kv_scale=True)
+    nsplit, fused = plan(m, 3)
+    assert fused == 2, "batched gate/up did not apply the SiLU gate in the same launch"
+    h = _hidden(m, 22, rows=3)
+    pos = 40
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(3, -1)
+    assert np.all(np.isfinite(logits))
+    _, want, n, total = oracle_batch_forced(m, h.numpy().reshape(3, -1), pos)
+    assert n <= 0.05 * total, f"{n} of {total} KV codes differ"
+    for b in range(3):
+        assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
+
+
 def test_qwen3_width_batch8_split_partials_summed_in_consumers_bit_exact(dev):
     """Batch 8 at full width: the split-K partials of the qkv, o and down
     projections summed by the kernels that consume them (attention prologue,
