@@ -567,8 +567,16 @@ constexpr int kInFlight = 2;
 struct Throttle {
   hipEvent_t ev[kInFlight] = {};
   bool on = false;
-  int init(int64_t steps) {
+  // off for runs of at most kInFlight steps and on a stream being captured
+  // (no host wait can order captured work)
+  int init(int64_t steps, hipStream_t s) {
     if (steps <= kInFlight) return R4Q_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {  // e.g. the null stream during a capture
+      (void)hipGetLastError();
+      return R4Q_OK;
+    }
+    if (cs != hipStreamCaptureStatusNone) return R4Q_OK;
     for (hipEvent_t& e : ev) R4Q_HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     on = true;
     return R4Q_OK;
@@ -631,7 +639,7 @@ int replay(r4q_ctx* ctx, hipStream_t st, std::vector<uint8_t> key, int* state, i
     }
   }
   Throttle th;
-  if (rc == R4Q_OK) rc = th.init(reps);
+  if (rc == R4Q_OK) rc = th.init(reps, gc.stream);
   for (int64_t t = 0; rc == R4Q_OK && t < reps; ++t) {
     rc = th.wait(t);
     if (rc != R4Q_OK) break;
@@ -748,7 +756,7 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
   R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
   if (!use_graph) {
     Throttle th;
-    R4Q_TRY(th.init(num_tokens));
+    R4Q_TRY(th.init(num_tokens, st));
     for (int64_t t = 0; t < num_tokens; ++t) {
       const int64_t pos = start_pos + t;
       R4Q_TRY(th.wait(t));
