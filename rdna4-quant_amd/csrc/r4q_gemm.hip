@@ -1242,7 +1242,9 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   float* part = S > 1 ? static_cast<float*>(ws) : nullptr;
   const dim3 grid((unsigned)(ntiles * S));
   const bool m8 = M <= 8;
-  if (silu_I > 0 && S == 1) {  // unsplit: the SiLU gate in the epilogue (M <= 8, caller)
+  if (silu_I > 0 && S == 1) {  // unsplit: the SiLU gate in the epilogue
+    R4Q_REQUIRE(M <= 8 && silu_I % 32 == 0 && N == 2 * silu_I,
+                "gate_up_silu: the unsplit epilogue takes at most 8 rows (M=%lld)", (long long)M);
 #define R4Q_SKINNY_SILU(WB)                                                                      \
   hipLaunchKernelGGL((gemm_skinny_kernel<WB, 8, true>), dim3((unsigned)(silu_I / 32)), dim3(256), \
                      0, st, xp, wp, sp, yp, nullptr, (int)M, (int)N, (int)K,                     \
