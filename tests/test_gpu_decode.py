@@ -78,6 +78,26 @@ def test_qwen3_width_batch8_step_vs_oracle(dev):
         assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
 
 
+def test_qwen3_width_batch8_ctx2048_step_vs_oracle(dev):
+    """Batch 8 at ctx 2048 (position 2048, cache capacity 2088): 8 attention
+    splits per (sequence, KV head) whose prologue sums the qkv split partials,
+    INT4 and INT8 layers; every row against the oracle under KV teacher
+    forcing."""
+    bits = {(0, "qkv"): 8, (1, "o"): 8}
+    m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=1024, max_seq=2088, seed=25,
+              bits=bits, batch=8, fill=2048, kv_scale=True)
+    nsplit, fused = plan(m, 8)
+    assert nsplit == 8 and fused == 2, (nsplit, fused)
+    h = _hidden(m, 26, rows=8)
+    pos = 2048
+    logits = step_logits(m, h.to(dev), pos).cpu().float().numpy().reshape(8, -1)
+    assert np.all(np.isfinite(logits))
+    _, want, n, total = oracle_batch_forced(m, h.numpy().reshape(8, -1), pos)
+    assert n <= 0.05 * total, f"{n} of {total} KV codes differ"
+    for b in range(8):
+        assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
+
+
 def test_qwen3_width_batch3_step_vs_oracle(dev):
     """Batch 3 at full width: gate_up runs unsplit with the SiLU gate in the
     skinny GEMM's epilogue on 3 of its 8 activation rows (the rest repeat the
