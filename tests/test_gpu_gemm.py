@@ -174,8 +174,6 @@ def test_gemm_silu_fwht_matches_gemm_then_silu(dev, bits, M, I, K, split):
     and, for M <= 8, without one (the unsplit GEMM over tiles of 32 gate rows
     and the 32 up rows of the same indices, the gate in its epilogue)."""
     import r4q_lib as R
-    if not split and M > 8:
-        pytest.skip("above 8 rows the gate needs the split path")
     g = S.gen(7 * M + I + K + bits)
     w, sz = S.weight(2 * I, K, bits, g)
     wd = w.to(dev)
@@ -186,6 +184,14 @@ def test_gemm_silu_fwht_matches_gemm_then_silu(dev, bits, M, I, K, split):
     ws = torch.empty(b.value if split else 0, dtype=torch.uint8, device=dev)
     wsp = ws.data_ptr() if split else None
     st = R.stream_handle()
+    if not split and M > 8:  # above 8 rows the gate needs the split path: rejected
+        x = torch.zeros(M, K, dtype=torch.float16, device=dev)
+        y = torch.empty(M, I, dtype=torch.float16, device=dev)
+        with pytest.raises(RuntimeError):
+            R.call("r4q_gemm_silu_fwht_ws", x.data_ptr(), wd.data_ptr(),
+                   None if sd is None else sd.data_ptr(), y.data_ptr(), M, I, K, bits, None, 0,
+                   st)
+        return
     for rep in range(2):
         x = (torch.randn(M, K, generator=g) * (0.5 + rep)).half().to(dev)
         gu = torch.empty(M, 2 * I, dtype=torch.float16, device=dev)
