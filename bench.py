@@ -18,8 +18,14 @@ Also measured in the same run:
   * engine_ms_per_token: the engine's own per-token loop (embedding,
     decode_step_logits, argmax, .item()).
 
+  * config4_matrix: the same hipGraph step at ctx 128 and 2048, batch 1
+    and 8 (the headline cell reused), each with KV caches of its own
+    capacity.
+A secondary leg that fails on the host is recorded under "errors" and the
+line is still printed.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 2048]
-       [--batch 1] [--no-cpu-baseline]
+       [--batch 1] [--no-cpu-baseline] [--no-matrix]
 """
 from __future__ import annotations
 
@@ -62,17 +68,131 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_model(ctx, extra, batch, dev):
+# The engine leg's per-token loop: untimed and timed tokens from ctx.
+ENGINE_WARM, ENGINE_TOKENS = 4, 32
+# Config-4 matrix (ctx 128 and 2048, batch 1 and 8).
+MATRIX_CTX = (128, 2048)
+MATRIX_BATCH = (1, 8)
+# Rows of the prompt pass (config 3's M); its RoPE rows come from the tables.
+PROMPT_M = 512
+
+
+def decode_ranges(ctx, steps, warmup):
+    """Position ranges (first, count) that the decode legs at context `ctx`
+    write into the KV cache: the warm-up replays (ending just before ctx, so
+    the timed steps start at ctx), the timed steps, and the engine leg."""
+    wpos = max(0, ctx - warmup)
+    out = [(ctx, steps), (ctx, ENGINE_WARM + ENGINE_TOKENS)]
+    if warmup > 0:
+        out.append((wpos, warmup))
+    return out
+
+
+def cache_capacity(ctx, steps, warmup):
+    """KV cache capacity for the decode legs at `ctx`: every position they
+    write plus 16 spare rows, as the reference sizes its graph bench's cache
+    (KVCache(ctx + n_tokens + 16), int4_engine_v5.py:555)."""
+    return max(first + count for first, count in decode_ranges(ctx, steps, warmup)) + 16
+
+
+def check_capacity(m_cap, ranges, what):
+    for first, count in ranges:
+        if first + count > m_cap:
+            raise RuntimeError(f"{what}: positions {first}..{first + count - 1} exceed the KV "
+                               f"cache capacity {m_cap}")
+
+
+def guarded(name, errors, fn, *a, **kw):
+    """Runs one secondary leg; a host-side failure is recorded in `errors`
+    (and the JSON line still printed) instead of ending the run."""
+    try:
+        return fn(*a, **kw)
+    except Exception as e:  # noqa: BLE001 - the record keeps the text
+        log(f"{name} failed: {type(e).__name__}: {e}")
+        errors[name] = f"{type(e).__name__}: {e}"
+        return None
+
+
+def build_model(ctx, extra, batch, dev, rope_len=0):
     import r4q_synth as S
-    m = S.qwen3_model(ctx, extra, batch, dev, log=log)
+    m = S.qwen3_model(ctx, extra, batch, dev, log=log, rope_len=rope_len)
     import torch
     torch.cuda.synchronize()
     return m
 
 
-def bench_args(m, start_pos):
+def bench_args(m, start_pos, caches=None):
     import r4q_synth as S
-    return S.qwen3_bench_args(m, start_pos)
+    return S.qwen3_bench_args(m, start_pos, caches)
+
+
+def timed_decode(m, h, steps, warmup, ctx, caches=None):
+    """`warmup` untimed graph-replayed greedy steps ending just before `ctx`
+    (the graph is captured there), then `steps` timed ones from `ctx`;
+    returns the timed seconds (host clock around the replays, both sides
+    synchronised)."""
+    import torch
+
+    import int4_hip
+    # Python's cyclic garbage collector stays out of the timed region (a
+    # generation-2 pass over the model's objects takes ~40 ms of host time
+    # in which no step is enqueued), as in timeit; it runs before the
+    # warm-up, so that the timed steps follow the warm-up with no idle gap
+    gc.collect()
+    gc.disable()
+    try:
+        if warmup > 0:
+            int4_hip.decode_bench_graph(h, m["embed"], warmup,
+                                        *bench_args(m, max(0, ctx - warmup), caches))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        int4_hip.decode_bench_graph(h, m["embed"], steps, *bench_args(m, ctx, caches))
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+    finally:
+        gc.enable()
+
+
+def step_bytes_of(m, ctx, steps, batch):
+    """Bytes one decode step streams: weights (packed + 3 B per 32-element
+    block), the FP16 LM head and the KV cache at the timed steps' mean
+    length."""
+    kv = m["L"] * 2 * m["Hk"] * m["hd"] * (ctx + steps // 2) * batch
+    return m["wbytes"] + m["lm_bytes"] + kv
+
+
+def matrix_leg(m, dev, steps, warmup, headline=None):
+    """Config 4: the hipGraph decode step at ctx in MATRIX_CTX x batch in
+    MATRIX_BATCH, each cell with KV caches of its own capacity
+    (cache_capacity) over the model's weights, `warmup` untimed then
+    `steps` timed steps.  `headline` = (ctx, batch, seconds) of a cell
+    already measured with the model's own caches."""
+    import r4q_synth as S
+    import torch
+    cells = {}
+    g = S.gen(44, dev)
+    for ctx in MATRIX_CTX:
+        for batch in MATRIX_BATCH:
+            key = f"ctx{ctx}_b{batch}"
+            if headline is not None and headline[:2] == (ctx, batch):
+                dt = headline[2]
+            else:
+                cap = cache_capacity(ctx, steps, warmup)
+                check_capacity(cap, decode_ranges(ctx, steps, warmup), key)
+                caches = S.fp8_caches(m["L"], m["Hk"], m["hd"], ctx, cap, batch, g, dev)
+                h = (torch.randn(batch, 1, m["D"], generator=torch.Generator().manual_seed(1))
+                     * 0.5).half().to(dev)
+                dt = timed_decode(m, h, steps, warmup, ctx, caches)
+                del caches, h
+                torch.cuda.empty_cache()
+            ms = dt * 1e3 / steps
+            sb = step_bytes_of(m, ctx, steps, batch)
+            cells[key] = {"ctx": ctx, "batch": batch, "ms_per_step": round(ms, 4),
+                          "tok_s": round(batch * steps / dt, 2), "step_bytes": sb,
+                          "step_roofline_frac": round(sb / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+            log(f"config-4 matrix ctx={ctx} batch={batch}: {ms:.3f} ms/step, "
+                f"{batch * steps / dt:.1f} tok/s")
+    return cells
 
 
 def replay_timed(graph, reps, st, warm=4):
@@ -518,7 +638,7 @@ def cpu_baseline(m, ctx, reps=5):
             "config3": gemm}
 
 
-def engine_leg(m, ctx, tokens=32, warm=4):
+def engine_leg(m, ctx, tokens=ENGINE_TOKENS, warm=ENGINE_WARM):
     """The engine's per-token loop (int4_engine_v5.py:343-355): embedding,
     decode_step_logits, logits[0, 0].float().argmax(), .item(), position + 1.
     Returns ms per token over `tokens` tokens after `warm` untimed ones."""
@@ -526,6 +646,7 @@ def engine_leg(m, ctx, tokens=32, warm=4):
     import torch.nn.functional as F
 
     import int4_hip
+    check_capacity(m["max_seq"], [(ctx, warm + tokens)], "engine leg")
     args = list(bench_args(m, ctx))
     embed = m["embed"]
     nid = torch.ones(1, 1, dtype=torch.long, device=embed.device)
@@ -552,6 +673,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-matrix", action="store_true",
+                    help="skip the config-4 ctx x batch matrix")
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the config-3 prefill GEMM leg (the program the MFMA "
                          "counter runs profile)")
@@ -593,6 +716,7 @@ def main():
                           "gemv_gbps": round(alg / us / 1e3, 1), "read_floor_us": round(rf_us, 3),
                           "read_floor_bytes": rf_bytes, "copy_bytes": nbytes}), flush=True)
         return
+    errors = {}
     # the config-0 GEMV first, on a GPU not yet holding the 11 GB model
     us = alg = gbps = rf_us = None
     if not args.decode_only:
@@ -604,13 +728,17 @@ def main():
 
     attn = {}
     for c in (() if args.decode_only else (128, 2048, 8192, 32768)):
-        a_us, a_bytes = flash_decode_leg(dev, c)
+        r = guarded(f"flash_decode_{c}", errors, flash_decode_leg, dev, c)
+        if r is None:
+            continue
+        a_us, a_bytes = r
         attn[str(c)] = {"us": round(a_us, 3), "kv_bytes": a_bytes,
                         "gbps": round(a_bytes / a_us / 1e3, 1),
                         "frac": round(a_bytes / a_us / 1e3 / HBM_PEAK_GBPS, 4)}
         log(f"flash-decode ctx={c}: {a_us:.2f} us, {a_bytes / a_us / 1e3:.0f} GB/s (cold KV)")
     torch.cuda.empty_cache()
-    pgemm = {} if args.decode_only else prefill_gemm_leg(dev)
+    pgemm = {} if args.decode_only else (guarded("prefill_gemm", errors, prefill_gemm_leg, dev)
+                                         or {})
     for k, v in pgemm.items():
         rs = v["reference_strategy"]
         log(f"prefill GEMM 512x{k.replace('x', ' -> ')} INT4: {v['us']:.1f} us, "
@@ -620,36 +748,29 @@ def main():
     torch.cuda.empty_cache()
     layer = None
     if not args.decode_only:
-        l_us, l_bytes = layer_leg(dev, args.ctx)
-        layer = {"us": round(l_us, 3), "bytes": l_bytes, "gbps": round(l_bytes / l_us / 1e3, 1),
-                 "frac": round(l_bytes / l_us / 1e3 / HBM_PEAK_GBPS, 4)}
-        log(f"one decoder layer (qkv / o / gate_up INT4, down INT8, ctx={args.ctx}): "
-            f"{l_us:.1f} us, {l_bytes / l_us / 1e3:.0f} GB/s")
+        r = guarded("layer", errors, layer_leg, dev, args.ctx)
+        if r is not None:
+            l_us, l_bytes = r
+            layer = {"us": round(l_us, 3), "bytes": l_bytes,
+                     "gbps": round(l_bytes / l_us / 1e3, 1),
+                     "frac": round(l_bytes / l_us / 1e3 / HBM_PEAK_GBPS, 4)}
+            log(f"one decoder layer (qkv / o / gate_up INT4, down INT8, ctx={args.ctx}): "
+                f"{l_us:.1f} us, {l_bytes / l_us / 1e3:.0f} GB/s")
         torch.cuda.empty_cache()
 
     log("building synthetic model")
     t0 = time.time()
-    # capacity for the decode steps and for the 512-token prompt leg below
-    m = build_model(args.ctx, max(args.warmup + args.steps + 8, 520 - args.ctx), args.batch, dev)
+    # KV capacity for every position the decode legs at ctx write
+    # (decode_ranges); RoPE rows also for the prompt pass
+    cap = cache_capacity(args.ctx, args.steps, args.warmup)
+    m = build_model(args.ctx, cap - args.ctx, args.batch, dev, rope_len=PROMPT_M)
+    check_capacity(m["max_seq"], decode_ranges(args.ctx, args.steps, args.warmup), "decode")
     log(f"model ready in {time.time() - t0:.1f} s (weights {m['wbytes'] / 1e9:.2f} GB + "
-        f"LM head {m['lm_bytes'] / 1e9:.2f} GB)")
+        f"LM head {m['lm_bytes'] / 1e9:.2f} GB, KV capacity {m['max_seq']})")
     h = (torch.randn(args.batch, 1, m["D"], generator=torch.Generator().manual_seed(1)) * 0.5).half().to(dev)
 
-    # Python's cyclic garbage collector stays out of the timed region (a
-    # generation-2 pass over the model's objects takes ~40 ms of host time
-    # in which no step is enqueued), as in timeit; it runs before the
-    # warm-up, so that the timed steps follow the warm-up with no idle gap
-    gc.collect()
-    gc.disable()
-    # warm-up: capture and replay from ctx - warmup so the timed steps start at ctx
-    wpos = args.ctx - args.warmup
-    int4_hip.decode_bench_graph(h, m["embed"], args.warmup, *bench_args(m, wpos))
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    int4_hip.decode_bench_graph(h, m["embed"], args.steps, *bench_args(m, args.ctx))
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    gc.enable()
+    # warm-up replays end just before ctx, so the timed steps start at ctx
+    dt = timed_decode(m, h, args.steps, args.warmup, args.ctx)
     log(f"warm-up {args.warmup} steps done before the timed ones")
     ms = dt * 1000.0 / args.steps
     tok_s = args.batch * args.steps / dt
@@ -657,49 +778,31 @@ def main():
     eng_ms = None
     if args.batch == 1:
         gc.disable()
-        eng_ms = engine_leg(m, args.ctx)
+        eng_ms = guarded("engine", errors, engine_leg, m, args.ctx)
         gc.enable()
-        log(f"engine loop (decode_step_logits + argmax + .item()): {eng_ms:.3f} ms/token")
+        if eng_ms is not None:
+            log(f"engine loop (decode_step_logits + argmax + .item()): {eng_ms:.3f} ms/token")
     if args.decode_only:
         print(json.dumps({"ms_per_step": round(ms, 4), "tok_s": round(tok_s, 3),
-                          "ctx": args.ctx, "batch": args.batch}), flush=True)
+                          "ctx": args.ctx, "batch": args.batch, "engine_ms_per_token": eng_ms,
+                          "errors": errors or None}), flush=True)
         return
+    matrix = None
+    if not args.no_matrix:
+        matrix = guarded("matrix", errors, matrix_leg, m, dev, args.steps, args.warmup,
+                         (args.ctx, args.batch, dt))
 
     # prompt pass: 512 tokens through all layers + LM head for every row
     # (config 3's GEMM shapes inside the full prefill)
-    pre_m = 512
-    ids = torch.randint(0, m["V"], (pre_m,), generator=torch.Generator().manual_seed(3)).to(dev)
-    pre_args = bench_args(m, 0)
-    lay = pre_args[:18] + pre_args[19:25]  # layer block without the position
-    had = pre_args[-1]
-    # the garbage collector runs before two untimed passes (run between them
-    # and the timed ones, its ~40 ms idle gap left the first timed pass ~9%
-    # slower: 23.6 against 21.6-21.9 ms), then the median of five timed passes
-    gc.collect()
-    gc.disable()
-    for _ in range(2):
-        int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"],
-                                m["D"], *lay, had)
-    torch.cuda.synchronize()
-    runs = []
-    for _ in range(5):
-        t0 = time.perf_counter()
-        int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"],
-                                m["D"], *lay, had)
-        torch.cuda.synchronize()
-        runs.append(time.perf_counter() - t0)
-    pre_s = sorted(runs)[2]
-    gc.enable()
-    log(f"prefill {pre_m} tokens: {pre_s * 1e3:.1f} ms, {pre_m / pre_s:.0f} tok/s (runs "
-        f"{', '.join(f'{r * 1e3:.1f}' for r in runs)} ms)")
+    pre_s = guarded("prefill", errors, prompt_leg, m, dev)
 
-    kv_bytes = m["L"] * 2 * m["Hk"] * m["hd"] * (args.ctx + args.steps // 2) * args.batch
-    step_bytes = m["wbytes"] + m["lm_bytes"] + kv_bytes
+    step_bytes = step_bytes_of(m, args.ctx, args.steps, args.batch)
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the reference's torch path on the host CPU")
-        cpu = cpu_baseline(m, args.ctx)
-        log(f"cpu baseline: {cpu['value']} tok/s")
+        cpu = guarded("cpu_baseline", errors, cpu_baseline, m, args.ctx)
+        if cpu is not None:
+            log(f"cpu baseline: {cpu['value']} tok/s")
 
     out = {
         "metric": METRIC,
@@ -720,13 +823,13 @@ def main():
                          "FP8 E4M3 KV"),
             "hidden": m["D"], "intermediate": m["I"], "heads": m["H"], "kv_heads": m["Hk"],
             "head_dim": m["hd"], "layers": m["L"], "vocab": m["V"], "ctx": args.ctx,
-            "batch": args.batch,
+            "batch": args.batch, "kv_capacity": m["max_seq"],
         },
         "step_bytes": step_bytes,
         "step_gbps": round(step_bytes / (ms / 1e3) / 1e9, 1),
         "step_roofline_frac": round(step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
         "int4_gemv_gbps": round(gbps, 1),
-        "prefill_512_tok_s": round(pre_m / pre_s, 1),
+        "prefill_512_tok_s": None if pre_s is None else round(PROMPT_M / pre_s, 1),
         # the engine's own per-token path: eager decode_step_logits call (a
         # replayed graph inside), argmax and .item() per token, at ctx
         "engine_ms_per_token": None if eng_ms is None else round(eng_ms, 4),
@@ -745,6 +848,8 @@ def main():
             "read_floor_us": round(rf_us, 3),
             "frac_of_read_floor": round(rf_us / us, 4),
         },
+        # config 4: ctx x batch matrix of the hipGraph step (same steps / warm-up)
+        "config4_matrix": matrix,
         # config 1: one decoder layer's GEMVs + fusions (+ its attention) at batch 1
         "layer": layer,
         # config 2: flash-decode alone, batch 1, cold KV (ring > 512 MB), per ctx
@@ -752,8 +857,46 @@ def main():
         # config 3: prefill GEMM, M = 512, INT4, K x N, fraction of 2.5 PF fp16 MFMA
         "prefill_gemm": pgemm,
         "cpu_baseline": cpu,
+        "errors": errors or None,
     }
     print(json.dumps(out), flush=True)
+
+
+def prompt_leg(m, dev):
+    """A 512-token prompt through all layers + the LM head for every row
+    (prefill_logits); median seconds of five timed passes after two untimed
+    ones."""
+    import torch
+
+    import int4_hip
+    ids = torch.randint(0, m["V"], (PROMPT_M,),
+                        generator=torch.Generator().manual_seed(3)).to(dev)
+    pre_args = bench_args(m, 0)
+    lay = pre_args[:18] + pre_args[19:25]  # layer block without the position
+    had = pre_args[-1]
+    # the garbage collector runs before two untimed passes (run between them
+    # and the timed ones, its ~40 ms idle gap left the first timed pass ~9%
+    # slower: 23.6 against 21.6-21.9 ms), then the median of five timed passes
+    gc.collect()
+    gc.disable()
+    try:
+        for _ in range(2):
+            int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"],
+                                    m["D"], *lay, had)
+        torch.cuda.synchronize()
+        runs = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            int4_hip.prefill_logits(ids, m["embed"], m["final_norm"], m["lm_w"], None, m["V"],
+                                    m["D"], *lay, had)
+            torch.cuda.synchronize()
+            runs.append(time.perf_counter() - t0)
+    finally:
+        gc.enable()
+    pre_s = sorted(runs)[2]
+    log(f"prefill {PROMPT_M} tokens: {pre_s * 1e3:.1f} ms, {PROMPT_M / pre_s:.0f} tok/s (runs "
+        f"{', '.join(f'{r * 1e3:.1f}' for r in runs)} ms)")
+    return pre_s
 
 
 if __name__ == "__main__":

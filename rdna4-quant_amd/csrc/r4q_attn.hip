@@ -593,36 +593,6 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   return launch_status("flash_decode");
 }
 
-namespace {
-std::atomic<uint64_t> g_devbuf_epoch{0};
-}
-
-uint64_t devbuf_epoch() { return g_devbuf_epoch.load(std::memory_order_relaxed); }
-
-int DevBuf::reserve(size_t need) {
-  if (need <= bytes) return R4Q_OK;
-  g_devbuf_epoch.fetch_add(1, std::memory_order_relaxed);
-  if (ptr) {
-    (void)hipFree(ptr);
-    ptr = nullptr;
-    bytes = 0;
-  }
-  const size_t cap = (need + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
-  if (hipMalloc(&ptr, cap) != hipSuccess) {
-    ptr = nullptr;
-    return fail(R4Q_ENOMEM, "hipMalloc(%zu) failed", cap);
-  }
-  bytes = cap;
-  return R4Q_OK;
-}
-
-void DevBuf::release() {
-  if (ptr) g_devbuf_epoch.fetch_add(1, std::memory_order_relaxed);
-  if (ptr) (void)hipFree(ptr);
-  ptr = nullptr;
-  bytes = 0;
-}
-
 }  // namespace r4q
 
 extern "C" int r4q_flash_decode(r4q_ctx* ctx, const void* q, int64_t q_stride,

@@ -9,19 +9,17 @@
 
 namespace r4q {
 
-// A grow-only device buffer.
+// A grow-only device buffer.  Every (re)allocation and release adds one to
+// *epoch (the owning context's count), so that a captured graph, whose key
+// holds that count, is never replayed after one of its buffers could have
+// moved.
 struct DevBuf {
   void* ptr = nullptr;
   size_t bytes = 0;
+  uint64_t* epoch = nullptr;
   int reserve(size_t need);  // R4Q_OK / R4Q_ENOMEM; never called during capture
   void release();
 };
-
-// Number of DevBuf (re)allocations and releases so far in this process.  A
-// captured graph bakes in the addresses of the buffers it uses; its cache
-// key holds this count, so a graph is never replayed after any buffer could
-// have moved.
-uint64_t devbuf_epoch();
 
 struct GraphCache;  // captured decode steps (r4q_decode.hip)
 
@@ -29,6 +27,9 @@ struct GraphCache;  // captured decode steps (r4q_decode.hip)
 
 struct r4q_ctx {
   int device = -1;
+  // reallocations of this context's buffers (DevBuf::epoch); a graph key
+  // holds it, so growing another context's buffers invalidates no graph here
+  uint64_t buf_epoch = 0;
   r4q::DevBuf attn;      // flash-decode partials
   r4q::DevBuf step;      // decode-step activations
   r4q::DevBuf prefill;   // prefill activations
@@ -36,6 +37,9 @@ struct r4q_ctx {
   r4q::DevBuf sample;    // sampling tables (kept zeroed between calls)
   size_t sample_zeroed = 0;  // bytes of `sample` known to be zero
   r4q::GraphCache* graphs = nullptr;
+  r4q_ctx() {
+    for (r4q::DevBuf* b : {&attn, &step, &prefill, &misc, &sample}) b->epoch = &buf_epoch;
+  }
 };
 
 namespace r4q {

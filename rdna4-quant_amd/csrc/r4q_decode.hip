@@ -58,6 +58,9 @@ struct GraphCache {
       size_t lru = 0;
       for (size_t i = 1; i < entries.size(); ++i)
         if (entries[i].used < entries[lru].used) lru = i;
+      // replays of the evicted graph may still be queued on the stream
+      // (the decode loops return with up to kInFlight of them in flight)
+      (void)hipStreamSynchronize(stream);
       (void)hipGraphExecDestroy(entries[lru].exec);
       entries.erase(entries.begin() + (std::ptrdiff_t)lru);
     }
@@ -522,13 +525,13 @@ int check_positions(const r4q_model* m, int64_t first, int64_t count) {
 
 // Key of a captured graph: model struct, layer table, launch shape and every
 // buffer address the graph bakes in (the context's buffers, the sampling
-// workspace, the caller's token array), plus the buffer epoch, which moves
-// whenever any context buffer is reallocated.
-std::vector<uint8_t> graph_key(int kind, const r4q_model* m, int64_t B, int nsplit,
-                               const void* tokens_out, const Bufs& bf, const SampleCfg& scfg,
-                               const void* sample_ws) {
+// workspace, the caller's token array), plus the context's buffer epoch,
+// which moves whenever one of its buffers is reallocated.
+std::vector<uint8_t> graph_key(const r4q_ctx* ctx, int kind, const r4q_model* m, int64_t B,
+                               int nsplit, const void* tokens_out, const Bufs& bf,
+                               const SampleCfg& scfg, const void* sample_ws) {
   const void* extra[] = {tokens_out, bf.h, bf.attn, bf.state, bf.ws, sample_ws};
-  const uint64_t epoch = devbuf_epoch();
+  const uint64_t epoch = ctx->buf_epoch;
   // launch-shape overrides change what a step launches
   const Tuning& tu = tuning();
   const int knobs[] = {tu.gemv_lpr.load(),      tu.gemv_wgs.load(),    tu.gemv_ub.load(),
@@ -704,8 +707,8 @@ int decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
                           want_logits, gs);
     };
     R4Q_TRY(replay(ctx, st,
-                   graph_key(want_logits ? kGraphStep : -kGraphStep, m, B, nsplit, nullptr, bf,
-                             SampleCfg{0.f, 1.f, 0}, nullptr),
+                   graph_key(ctx, want_logits ? kGraphStep : -kGraphStep, m, B, nsplit, nullptr,
+                             bf, SampleCfg{0.f, 1.f, 0}, nullptr),
                    bf.state, (int)pos, 1, record));
   } else {
     R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, want_logits, st));
@@ -773,7 +776,7 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
                          gs));
     return enqueue_sample(m, dm, B, bf, toks, true, 0, gs, &scfg, sws);
   };
-  return replay(ctx, st, graph_key(kGraphLoop, m, B, nsplit, tokens_out, bf, scfg, sws),
+  return replay(ctx, st, graph_key(ctx, kGraphLoop, m, B, nsplit, tokens_out, bf, scfg, sws),
                 bf.state, (int)start_pos, num_tokens, record);
 }
 }  // namespace

@@ -73,6 +73,31 @@ Tuning& tuning() {
   return t;
 }
 
+int DevBuf::reserve(size_t need) {
+  if (need <= bytes) return R4Q_OK;
+  if (epoch) ++*epoch;
+  if (ptr) {
+    (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  const size_t cap = (need + 0xFFFFF) & ~(size_t)0xFFFFF;  // 1 MiB granules
+  if (hipMalloc(&ptr, cap) != hipSuccess) {
+    ptr = nullptr;
+    return fail(R4Q_ENOMEM, "hipMalloc(%zu) failed", cap);
+  }
+  bytes = cap;
+  return R4Q_OK;
+}
+
+void DevBuf::release() {
+  if (!ptr) return;
+  if (epoch) ++*epoch;
+  (void)hipFree(ptr);
+  ptr = nullptr;
+  bytes = 0;
+}
+
 }  // namespace r4q
 
 extern "C" const char* r4q_last_error(void) { return r4q::g_err; }

@@ -141,16 +141,33 @@ def random_kv_values(Hk: int, n_fill: int, hd: int, g: torch.Generator, device="
     return (torch.randn(batch, Hk, n_fill, hd, generator=g, device=device) * scale).half()
 
 
-def qwen3_model(ctx: int, extra: int, batch: int, device, log=None) -> dict:
+def fp8_caches(n_layers: int, Hk: int, hd: int, ctx: int, capacity: int, batch: int,
+               g: torch.Generator, device) -> tuple:
+    """Per-layer FP8 K and V caches uint8 [batch, Hk, capacity, hd] whose
+    positions [0, ctx) hold the reference encoder's codes of N(0,1) values
+    (the library's fp16_to_fp8) and the rest zeros."""
+    import int4_hip
+
+    kc, vc = [], []
+    for _ in range(n_layers):
+        k = torch.zeros(batch, Hk, capacity, hd, dtype=torch.uint8, device=device)
+        v = torch.zeros_like(k)
+        k[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
+        v[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
+        kc.append(k)
+        vc.append(v)
+    return kc, vc
+
+
+def qwen3_model(ctx: int, extra: int, batch: int, device, log=None, rope_len: int = 0) -> dict:
     """The BASELINE config-4 model, generated on `device`: 40 Qwen3-14B-shaped
     layers (seed 4; 32 of the 160 projection matrices INT8 by
     precision_mask), FP16 embedding and LM head, FP8 KV caches of capacity
     ctx + extra per layer with positions [0, ctx) holding the reference
-    encoder's codes of N(0,1) values (the library's fp16_to_fp8).  Returns a
-    dict with the int4_hip argument lists ("args"), caches ("kc", "vc"), RoPE
-    tables, final norm, LM head, embedding, dims and byte counts."""
-    import int4_hip
-
+    encoder's codes of N(0,1) values (the library's fp16_to_fp8).  The RoPE
+    tables have max(ctx + extra, rope_len) rows.  Returns a dict with the
+    int4_hip argument lists ("args"), caches ("kc", "vc"), RoPE tables, final
+    norm, LM head, embedding, dims and byte counts."""
     c = QWEN3_14B
     D, I, H, Hk, hd, L, V = c["hidden"], c["inter"], c["heads"], c["kv_heads"], c["head_dim"], \
         c["layers"], c["vocab"]
@@ -172,15 +189,8 @@ def qwen3_model(ctx: int, extra: int, batch: int, device, log=None) -> dict:
         if log and (li + 1) % 10 == 0:
             log(f"layer {li + 1}/{L} generated")
     max_seq = ctx + extra
-    kc, vc = [], []
-    for li in range(L):
-        k = torch.zeros(batch, Hk, max_seq, hd, dtype=torch.uint8, device=device)
-        v = torch.zeros_like(k)
-        k[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
-        v[:, :, :ctx] = int4_hip.fp16_to_fp8(random_kv_values(Hk, ctx, hd, g, device, batch))
-        kc.append(k)
-        vc.append(v)
-    cos, sin = rope_tables(hd, max_seq, c["rope_theta"], device)
+    kc, vc = fp8_caches(L, Hk, hd, ctx, max_seq, batch, g, device)
+    cos, sin = rope_tables(hd, max(max_seq, rope_len), c["rope_theta"], device)
     final_norm = norm_weight(D, g, device)
     lm_w, _ = fp16_weight(V, D, g, device)
     embed, _ = fp16_weight(V, D, g, device)
@@ -189,13 +199,17 @@ def qwen3_model(ctx: int, extra: int, batch: int, device, log=None) -> dict:
                 max_seq=max_seq, wbytes=wbytes, lm_bytes=V * D * 2)
 
 
-def qwen3_bench_args(m: dict, start_pos: int) -> tuple:
+def qwen3_bench_args(m: dict, start_pos: int, caches: tuple = None) -> tuple:
     """int4_hip decode_bench / decode_loop argument tail of a qwen3_model
-    (layer block at start_pos, caches, final norm, LM head, hadamard)."""
+    (layer block at start_pos, caches, final norm, LM head, hadamard);
+    `caches` = (k list, v list) replaces the model's own caches."""
     a = m["args"]
-    had = torch.zeros(32, 32, dtype=torch.float16, device=m["lm_w"].device)
+    kc, vc = caches if caches is not None else (m["kc"], m["vc"])
+    had = m.get("had")
+    if had is None:
+        had = m["had"] = torch.zeros(32, 32, dtype=torch.float16, device=m["lm_w"].device)
     return (a["qkv_w"], a["qkv_s"], a["qkv_N"], a["o_w"], a["o_s"], a["o_N"], a["gu_w"],
             a["gu_s"], a["gu_N"], a["down_w"], a["down_s"], a["down_N"], a["in_norm"],
             a["post_norm"], a["q_norm"], a["k_norm"], m["cos"], m["sin"], start_pos, m["H"],
-            m["Hk"], m["hd"], m["D"], m["I"], m["eps"], m["kc"], m["vc"], m["final_norm"],
+            m["Hk"], m["hd"], m["D"], m["I"], m["eps"], kc, vc, m["final_norm"],
             m["lm_w"], None, m["V"], m["D"], had)

@@ -140,3 +140,25 @@ def test_gate_up_silu_split_point():
     assert split(96) == 96
     with pytest.raises(RuntimeError):
         split(100)
+
+
+def test_model_cache_key_follows_storage_swaps():
+    # A tensor whose storage is swapped in place keeps its id(); the model
+    # cache key must still change (a stale key would point the kernels at
+    # the old storage).  Host-only: keys are built without device work.
+    import int4_hip
+    ws = [torch.zeros(8, dtype=torch.uint8) for _ in range(3)]
+    kc = [torch.zeros(1, 2, 16, 4, dtype=torch.uint8) for _ in range(3)]
+    args = [ws, [1, 2, 3], kc, 0.5]
+    k0 = int4_hip._key_of(args, shaped=(2,))
+    assert int4_hip._key_of(args, shaped=(2,)) == k0
+    ws[1].set_(torch.zeros(8, dtype=torch.uint8))  # new storage, same tensor object
+    k1 = int4_hip._key_of(args, shaped=(2,))
+    assert k1 != k0
+    kc[0].resize_(1, 2, 8, 4)  # shrinks in place: same pointer, other capacity
+    assert int4_hip._key_of(args, shaped=(2,)) != k1
+    # None entries (FP16 weights carry no scale table) are keyed too
+    kn = int4_hip._key_of([[None, ws[0]]])
+    assert kn == int4_hip._key_of([[None, ws[0]]])
+    ws[0].set_(torch.zeros(8, dtype=torch.uint8))
+    assert int4_hip._key_of([[None, ws[0]]]) != kn
