@@ -494,16 +494,23 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
   float M = -INFINITY, Ls = 0.f, a0 = 0.f, a1 = 0.f;
   for (int c0 = 0; c0 < nsplit; c0 += CH) {
     const int nc = min(CH, nsplit - c0);
-    float ms = -INFINITY, ls = 0.f;
-    if (lane < nc) {
-      ms = pb[(int64_t)(c0 + lane) * kPart];
-      ls = pb[(int64_t)(c0 + lane) * kPart + 1];
-    }
+    // (m, l) of split c0 + lane, loaded unconditionally from a clamped split
+    float2 ml = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(lane, nc - 1)) * kPart);
     float2 ov[CH];
 #pragma unroll
     for (int s = 0; s < CH; ++s)
       ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(s, nc - 1)) * kPart + 4 +
                                                2 * lane);
+    // Every load of the round precedes the first wait: the empty asm takes
+    // every loaded register.  Left to itself the compiler issued ~18 of the
+    // 34 loads, waited for (m, l), ran the max / exp and only then issued
+    // the rest (two memory round trips); a load under `lane < nc` was waited
+    // for on its own.  A memory clobber would not order these loads (the
+    // partials are read-only and restrict-qualified).
+    asm volatile("" : "+v"(ml.x), "+v"(ml.y));
+#pragma unroll
+    for (int s = 0; s < CH; ++s) asm volatile("" : "+v"(ov[s].x), "+v"(ov[s].y));
+    const float ms = lane < nc ? ml.x : -INFINITY, ls = lane < nc ? ml.y : 0.f;
     const float Mn = fmaxf(M, wave_max(ms));
     const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);  // rescale of earlier chunks
     const float w = (ms == -INFINITY) ? 0.f : __expf(ms - Mn);

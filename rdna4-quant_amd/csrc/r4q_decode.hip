@@ -43,6 +43,7 @@ struct GraphCache {
     uint64_t used = 0;
   };
   hipStream_t stream = nullptr;
+  hipEvent_t ev_in = nullptr, ev_out = nullptr;  // caller stream -> graph stream -> caller
   std::vector<Entry> entries;
   uint64_t clock = 0;
   hipGraphExec_t find(const std::vector<uint8_t>& key) {
@@ -68,6 +69,8 @@ struct GraphCache {
   }
   ~GraphCache() {
     for (Entry& e : entries) (void)hipGraphExecDestroy(e.exec);
+    if (ev_in) (void)hipEventDestroy(ev_in);
+    if (ev_out) (void)hipEventDestroy(ev_out);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -463,10 +466,19 @@ __global__ __launch_bounds__(256) void argmax_embed_kernel(
   for (int i = threadIdx.x; i < D / 8; i += blockDim.x) dst[i] = src[i];
 }
 
-__global__ void set_state_kernel(int* state, int pos) {
-  state[kPos] = pos;
-  state[kSeq] = pos + 1;
-  state[kStep] = 0;
+// Start of a replayed run: the device position / length / step counters,
+// and the caller's hidden states copied into the step's input buffer
+// (n16 16-byte pieces; one launch instead of a copy and a kernel).
+__global__ void prime_kernel(int* __restrict__ state, int pos, const u4_t* __restrict__ src,
+                             u4_t* __restrict__ dst, int64_t n16) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    state[kPos] = pos;
+    state[kSeq] = pos + 1;
+    state[kStep] = 0;
+  }
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
 }
 
 __global__ void advance_kernel(int* state) {
@@ -521,6 +533,18 @@ int check_positions(const r4q_model* m, int64_t first, int64_t count) {
               "decode: positions up to %lld exceed the RoPE table (%d rows)",
               (long long)(first + count - 1), m->rope_len);
   return R4Q_OK;
+}
+
+// Whether the caller's stream is being captured (a hipStreamIsCapturing
+// error, e.g. the null stream while another stream captures, counts as yes:
+// no replay is started then).
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
 }
 
 // Key of a captured graph: model struct, layer table, launch shape and every
@@ -608,16 +632,20 @@ struct Throttle {
 // kept under `key`.
 template <class Record>
 int replay(r4q_ctx* ctx, hipStream_t st, std::vector<uint8_t> key, int* state, int pos,
-           int64_t reps, const Record& record) {
+           const void* hidden_in, void* h, size_t hidden_bytes, int64_t reps,
+           const Record& record) {
   if (!ctx->graphs) ctx->graphs = new GraphCache();
   GraphCache& gc = *ctx->graphs;
   if (!gc.stream) R4Q_HIP_TRY(hipStreamCreateWithFlags(&gc.stream, hipStreamNonBlocking));
-  hipEvent_t ev;
-  R4Q_HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
-  (void)hipEventRecord(ev, st);
-  (void)hipStreamWaitEvent(gc.stream, ev, 0);
-  hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(1), 0, gc.stream, state, pos);
-  int rc = launch_status("set_state");
+  if (!gc.ev_in) R4Q_HIP_TRY(hipEventCreateWithFlags(&gc.ev_in, hipEventDisableTiming));
+  if (!gc.ev_out) R4Q_HIP_TRY(hipEventCreateWithFlags(&gc.ev_out, hipEventDisableTiming));
+  R4Q_HIP_TRY(hipEventRecord(gc.ev_in, st));
+  R4Q_HIP_TRY(hipStreamWaitEvent(gc.stream, gc.ev_in, 0));
+  const int64_t n16 = (int64_t)(hidden_bytes / 16);
+  const unsigned pblocks = (unsigned)std::min<int64_t>(64, std::max<int64_t>(1, (n16 + 255) / 256));
+  hipLaunchKernelGGL(prime_kernel, dim3(pblocks), dim3(256), 0, gc.stream, state, pos,
+                     static_cast<const u4_t*>(hidden_in), static_cast<u4_t*>(h), n16);
+  int rc = launch_status("prime");
   hipGraphExec_t exec = rc == R4Q_OK ? gc.find(key) : nullptr;
   if (rc == R4Q_OK && !exec) {
     hipGraph_t graph = nullptr;
@@ -650,9 +678,8 @@ int replay(r4q_ctx* ctx, hipStream_t st, std::vector<uint8_t> key, int* state, i
     if (e != hipSuccess) rc = fail(R4Q_EHIP, "hipGraphLaunch: %s", hipGetErrorString(e));
     else rc = th.mark(t, gc.stream);
   }
-  (void)hipEventRecord(ev, gc.stream);
-  (void)hipStreamWaitEvent(st, ev, 0);
-  (void)hipEventDestroy(ev);
+  (void)hipEventRecord(gc.ev_out, gc.stream);
+  (void)hipStreamWaitEvent(st, gc.ev_out, 0);
   return rc;
 }
 
@@ -696,8 +723,14 @@ int decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
   Bufs bf;
   R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
-  R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
+  const size_t hbytes = (size_t)B * dm.D * 2;
   const bool want_logits = logits != nullptr;
+  // a stream being captured by the caller records the eager launches
+  if (use_graph && capturing(st)) use_graph = false;
+  // the prime kernel of a replay copies the hidden states in 16-byte pieces
+  const bool h16 = (reinterpret_cast<uintptr_t>(hidden_in) & 15) == 0;
+  if (use_graph && !h16)
+    R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, hbytes, hipMemcpyDeviceToDevice, st));
   if (use_graph) {
     // the same step with the position read from device memory; one graph
     // serves every position (the attention split count depends only on the
@@ -709,8 +742,9 @@ int decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
     R4Q_TRY(replay(ctx, st,
                    graph_key(ctx, want_logits ? kGraphStep : -kGraphStep, m, B, nsplit, nullptr,
                              bf, SampleCfg{0.f, 1.f, 0}, nullptr),
-                   bf.state, (int)pos, 1, record));
+                   bf.state, (int)pos, hidden_in, bf.h, h16 ? hbytes : 0, 1, record));
   } else {
+    R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, hbytes, hipMemcpyDeviceToDevice, st));
     R4Q_TRY(enqueue_step(m, dm, B, pos, nullptr, nullptr, nsplit, bf, want_logits, st));
   }
   if (logits)
@@ -756,8 +790,9 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
   int64_t* toks = static_cast<int64_t*>(tokens_out);
   void* sws = nullptr;
   if (scfg.temperature > 0.f) R4Q_TRY(sample_reserve(ctx, B, st, &sws));
-  R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)B * dm.D * 2, hipMemcpyDeviceToDevice, st));
+  const size_t hbytes = (size_t)B * dm.D * 2;
   if (!use_graph) {
+    R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, hbytes, hipMemcpyDeviceToDevice, st));
     Throttle th;
     R4Q_TRY(th.init(num_tokens, st));
     for (int64_t t = 0; t < num_tokens; ++t) {
@@ -776,8 +811,10 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
                          gs));
     return enqueue_sample(m, dm, B, bf, toks, true, 0, gs, &scfg, sws);
   };
+  const bool h16 = (reinterpret_cast<uintptr_t>(hidden_in) & 15) == 0;
+  if (!h16) R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, hbytes, hipMemcpyDeviceToDevice, st));
   return replay(ctx, st, graph_key(ctx, kGraphLoop, m, B, nsplit, tokens_out, bf, scfg, sws),
-                bf.state, (int)start_pos, num_tokens, record);
+                bf.state, (int)start_pos, hidden_in, bf.h, h16 ? hbytes : 0, num_tokens, record);
 }
 }  // namespace
 }  // namespace r4q

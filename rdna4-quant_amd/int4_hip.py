@@ -358,11 +358,10 @@ def _decode_common(hidden_in, layer_args, k_caches, v_caches, final=None, embed=
 
 
 def _step_entry(use_graph):
-    """The C entry point of one decode step: the graph-replayed step unless
-    the caller is capturing torch's stream itself (or asks for eager)."""
-    if use_graph is None:
-        use_graph = not torch.cuda.is_current_stream_capturing()
-    return "r4q_decode_step_graph" if use_graph else "r4q_decode_step"
+    """The C entry point of one decode step: the graph-replayed step (which
+    runs the eager launches itself when the caller is capturing the stream)
+    unless the caller asks for eager."""
+    return "r4q_decode_step" if use_graph is False else "r4q_decode_step_graph"
 
 
 def decode_step(hidden_in, qkv_w, qkv_s, qkv_N, o_w, o_s, o_N, gu_w, gu_s, gu_N, down_w, down_s,
