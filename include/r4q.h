@@ -44,9 +44,10 @@
  *   r4q_flash_decode     <- launch_flash_decode     (:1547-1593)
  *   r4q_flash_decode_qkv <- head_rmsnorm_rope_kv + launch_flash_decode
  *                           pair of the decode step (:1620-1683, :2487-2500)
- *   r4q_decode_step      <- decode_step / decode_step_logits (:2343-2595)
- *   r4q_decode_step_graph <- the same, as called once per token by the engine
- *                           (int4_engine_v5.py:272), replayed from a hipGraph
+ *   r4q_decode_step      <- decode_step / decode_step_logits (:2343-2595),
+ *                           as called once per token by the engine
+ *                           (int4_engine_v5.py:272)
+ *   r4q_decode_step_graph <- the same, replayed from a hipGraph
  *   r4q_decode_bench     <- decode_bench / decode_bench_graph (:2601-3041),
  *                           and decode_loop (:3284-3466) via tokens_out
  *   r4q_decode_profile   <- decode_profile          (:3047-3273)
@@ -329,9 +330,11 @@ R4Q_API int r4q_decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden
  * (model, B, buffers) combination captures the step with the position held
  * in device memory, later calls at any position set that position and replay
  * it (about 250 launches become one).  Bit-identical results to
- * r4q_decode_step.  Replaces the per-token decode_step_logits call of the
- * engine (int4_engine_v5.py:272 -> hip:2534-2595).  Must not be called while
- * the caller's stream is being captured. */
+ * r4q_decode_step.  On a stream that the caller is capturing it records the
+ * eager launches instead.  A caller that waits for every token before the
+ * next (the engine's per-token decode_step_logits, int4_engine_v5.py:272 ->
+ * hip:2534-2595) is faster with r4q_decode_step: the GPU starts on the
+ * first eager launch, but on a replay only once hipGraphLaunch returns. */
 R4Q_API int r4q_decode_step_graph(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in,
                                   int64_t B, int64_t pos, void* hidden_out, void* logits,
                                   void* stream);
