@@ -105,10 +105,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 
   __shared__ __align__(16) uint16_t qs[NORMQ ? G : 1][128];
   __shared__ __align__(16) uint8_t knew[128], vnew[128];
-  __shared__ float wst[4][G][2];                  // per wave: max, sum
-  __shared__ __align__(16) float wo[4][G][128];  // per wave: unnormalised O
-  __shared__ __align__(16) float ostage[G][128];
-  __shared__ float fin[G][2];  // merged max, sum
+  __shared__ float wst[4][G][2];  // per wave: max, sum
+  // per wave: unnormalised O in the MFMA output layout (see the epilogue);
+  // only the lane groups holding heads < G
+  constexpr int kOGroups = (G + 3) / 4;
+  __shared__ __align__(16) f4_t wo[4][8][16 * kOGroups];
 
   // wave index as a scalar: the chunk loops and the per-chunk guards are
   // then scalar branches (an MFMA computes its whole tile whatever EXEC holds)
@@ -395,82 +396,92 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     for (int c = wave + 4; c < nchunk; c += 4) step(kr0, vr0, c, c + 4);
   }
 
-  // ---- merge the 4 waves (each: max and sum per head, O rows per head)
+  // ---- merge the 4 waves.  Lane (col, g) holds O[head 4g + r][dim 8 col + j]
+  // in o[j][r]; every wave leaves its O and its (max, sum) per head in LDS,
+  // then wave w finishes component r = w, i.e. head 4g + w of each lane
+  // group: the waves' O combined in wave order (e^(m_w - M) weights, as one
+  // fma chain from 0), scaled, FWHT-32 across the lane's 8 dims (index bits
+  // 0-2) and the 4 lanes of its quad (bits 3-4: dims 32q .. 32q+31 sit in
+  // cols 4q .. 4q+3), i.e. the butterflies of fwht32 on the same values, in
+  // the same order.
   float lsum = l_run + __shfl_xor(l_run, 16);
   lsum += __shfl_xor(lsum, 32);
   if (g == 0 && col < G) {
     wst[wave][col][0] = m_run;
     wst[wave][col][1] = lsum;
   }
+  if (g < kOGroups) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = 4 * g + r;
-    if (h < G) {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) wo[wave][h][8 * col + d] = o[d][r];
-    }
+    for (int j = 0; j < 8; ++j) wo[wave][j][lane] = o[j];
   }
   __syncthreads();
+  const int h = 4 * g + wave;
+  if (h >= G) return;  // no global stores follow for this lane
+  float mw[4], lw[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = wst[w][h][0];
+    lw[w] = wst[w][h][1];
+  }
+  float M = mw[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) M = fmaxf(M, mw[w]);
+  float ew[4], l = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    ew[w] = (mw[w] == -INFINITY) ? 0.f : __expf(mw[w] - M);
+    l = __builtin_fmaf(ew[w], lw[w], l);
+  }
   const float oscale = vs;
-  for (int e = t; e < G * 128; e += 256) {
-    const int h = e >> 7, d = e & 127;
-    float M = wst[0][h][0];
+  float v[8];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) M = fmaxf(M, wst[w][h][0]);
-    float acc = 0.f, l = 0.f;
+  for (int j = 0; j < 8; ++j) {
+    float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = wst[w][h][0];
-      const float ew = (mw == -INFINITY) ? 0.f : __expf(mw - M);
-      acc = __builtin_fmaf(ew, wo[w][h][d], acc);
-      l = __builtin_fmaf(ew, wst[w][h][1], l);
-    }
-    ostage[h][d] = acc * oscale;
-    if (d == 0) {
-      fin[h][0] = M;
-      fin[h][1] = l;
-    }
+    for (int w = 0; w < 4; ++w) acc = __builtin_fmaf(ew[w], wo[w][j][lane][wave], acc);
+    v[j] = acc * oscale;
   }
-  __syncthreads();
-
-  // ---- one thread per 32-dim chunk: FWHT-32 (linear, so it commutes with
-  // the split merge), then the final fp16 output (single split) or the fp32
-  // partial (m, l, o)
-  if (t < 4 * G) {
-    const int h = t >> 2, cq = t & 3;
-    float v[32];
+  if (fwht) {
 #pragma unroll
-    for (int i = 0; i < 32; i += 4) {
-      const f4_t x = *reinterpret_cast<const f4_t*>(&ostage[h][32 * cq + i]);
-      v[i] = x[0];
-      v[i + 1] = x[1];
-      v[i + 2] = x[2];
-      v[i + 3] = x[3];
+    for (int step = 1; step < 8; step <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 8; i += 2 * step) {
+#pragma unroll
+        for (int jj = i; jj < i + step; ++jj) {
+          const float a = v[jj], bb = v[jj + step];
+          v[jj] = a + bb;
+          v[jj + step] = a - bb;
+        }
+      }
     }
-    if (fwht) fwht32(v);
-    if (nsplit == 1) {
-      const float l = fin[h][1];
-      const float inv = l > 0.f ? 1.0f / l : 0.f;
-      uint16_t* dst = outp + b * out_stride + (int64_t)(kh * G + h) * 128 + 32 * cq;
+    const bool hi1 = (col & 1) != 0, hi2 = (col & 2) != 0;
 #pragma unroll
-      for (int i = 0; i < 32; i += 8) {
-        u4_t w;
+    for (int j = 0; j < 8; ++j) {
+      const float x1 = dpp<kDppQuadXor1>(v[j]);
+      v[j] = hi1 ? x1 - v[j] : v[j] + x1;
+    }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          w[j] = (uint32_t)f2h(v[i + 2 * j] * inv) | ((uint32_t)f2h(v[i + 2 * j + 1] * inv) << 16);
-        *reinterpret_cast<u4_t*>(dst + i) = w;
-      }
-    } else {
-      float* dst = part + ((b * H + (int64_t)kh * G + h) * nsplit + sp) * kPart;
+    for (int j = 0; j < 8; ++j) {
+      const float x2 = dpp<kDppQuadXor2>(v[j]);
+      v[j] = hi2 ? x2 - v[j] : v[j] + x2;
+    }
 #pragma unroll
-      for (int i = 0; i < 32; i += 4) {
-        const f4_t x = {v[i], v[i + 1], v[i + 2], v[i + 3]};
-        *reinterpret_cast<f4_t*>(dst + 4 + 32 * cq + i) = x;
-      }
-      if (cq == 0) {
-        dst[0] = fin[h][0];
-        dst[1] = fin[h][1];
-      }
+    for (int j = 0; j < 8; ++j) v[j] *= kInvSqrt32;
+  }
+  if (nsplit == 1) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    u4_t w;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      w[jj] = (uint32_t)f2h(v[2 * jj] * inv) | ((uint32_t)f2h(v[2 * jj + 1] * inv) << 16);
+    *reinterpret_cast<u4_t*>(outp + b * out_stride + (int64_t)(kh * G + h) * 128 + 8 * col) = w;
+  } else {
+    float* dst = part + ((b * H + (int64_t)kh * G + h) * nsplit + sp) * kPart;
+    *reinterpret_cast<f4_t*>(dst + 4 + 8 * col) = f4_t{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f4_t*>(dst + 8 + 8 * col) = f4_t{v[4], v[5], v[6], v[7]};
+    if (col == 0) {
+      dst[0] = M;
+      dst[1] = l;
     }
   }
 }
