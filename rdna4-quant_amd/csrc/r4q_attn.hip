@@ -106,10 +106,11 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   __shared__ __align__(16) uint16_t qs[NORMQ ? G : 1][128];
   __shared__ __align__(16) uint8_t knew[128], vnew[128];
   __shared__ float wst[4][G][2];  // per wave: max, sum
-  // per wave: unnormalised O in the MFMA output layout (see the epilogue);
-  // only the lane groups holding heads < G
+  // per wave: unnormalised O by (component r, dims 8 col + 0..3 / 4..7,
+  // lane) of the MFMA output layout (see the epilogue); only the lane groups
+  // holding heads < G
   constexpr int kOGroups = (G + 3) / 4;
-  __shared__ __align__(16) f4_t wo[4][8][16 * kOGroups];
+  __shared__ __align__(16) f4_t wo[4][4][2][16 * kOGroups];
 
   // wave index as a scalar: the chunk loops and the per-chunk guards are
   // then scalar branches (an MFMA computes its whole tile whatever EXEC holds)
@@ -412,7 +413,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   }
   if (g < kOGroups) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) wo[wave][j][lane] = o[j];
+    for (int r = 0; r < 4; ++r) {
+      wo[wave][r][0][lane] = f4_t{o[0][r], o[1][r], o[2][r], o[3][r]};
+      wo[wave][r][1][lane] = f4_t{o[4][r], o[5][r], o[6][r], o[7][r]};
+    }
   }
   __syncthreads();
   const int h = 4 * g + wave;
@@ -433,12 +437,18 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     l = __builtin_fmaf(ew[w], lw[w], l);
   }
   const float oscale = vs;
+  f4_t ow[4][2];  // component r = wave of every wave's O
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    ow[w][0] = wo[w][wave][0][lane];
+    ow[w][1] = wo[w][wave][1][lane];
+  }
   float v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) acc = __builtin_fmaf(ew[w], wo[w][j][lane][wave], acc);
+    for (int w = 0; w < 4; ++w) acc = __builtin_fmaf(ew[w], ow[w][j >> 2][j & 3], acc);
     v[j] = acc * oscale;
   }
   if (fwht) {
@@ -454,17 +464,14 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
         }
       }
     }
-    const bool hi1 = (col & 1) != 0, hi2 = (col & 2) != 0;
+    // partner p, own value u: the lower lane keeps u + p, the upper p - u,
+    // both as fma(+-1, u, p) (an exact product, one rounding: the same
+    // values as the add and subtract)
+    const float s1 = (col & 1) ? -1.0f : 1.0f, s2 = (col & 2) ? -1.0f : 1.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float x1 = dpp<kDppQuadXor1>(v[j]);
-      v[j] = hi1 ? x1 - v[j] : v[j] + x1;
-    }
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s1, v[j], dpp<kDppQuadXor1>(v[j]));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float x2 = dpp<kDppQuadXor2>(v[j]);
-      v[j] = hi2 ? x2 - v[j] : v[j] + x2;
-    }
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(s2, v[j], dpp<kDppQuadXor2>(v[j]));
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= kInvSqrt32;
   }
