@@ -493,59 +493,65 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   }
 }
 
-// Split merge, one wave per (query head, sequence); lane j owns dims 2j and
-// 2j+1.  Every load is issued before any arithmetic:
+// Split merge, one wave per (query head, sequence):
 //   m* = max_s m_s,  out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s.
-// CH splits per round (16, 32 or 64: the smallest covering the split count;
-// the slots past the last split add exact zeros, so CH does not change the
-// result).  Measured: 16 splits 4.56 us with CH = 64, 2.24 us with CH = 16.
+// The two half-waves take the even and the odd splits, lane j of a half
+// owning dims 4j .. 4j+3 (16-byte loads: one instruction reads two splits'
+// o), and add their sums at the end.  CH splits per round (16, 32 or 64:
+// the smallest covering the split count) with a running maximum; every load
+// of a round is issued before any arithmetic; slots past the last split
+// re-read it and get weight 0, so CH does not change the result.
 template <int CH>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part,
                                                         uint16_t* __restrict__ outp,
                                                         int64_t out_stride, int H, int nsplit) {
+  static_assert(CH % 2 == 0 && CH <= 64, "two splits per load, one (m, l) per lane");
   const int h = blockIdx.x;
   const int64_t b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x, hh = lane >> 5, j = lane & 31;
   const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
-  // splits in chunks of 64 (lane s holds split c0+s's m and l) with a
-  // running maximum; every load of a chunk is issued before its arithmetic
-  float M = -INFINITY, Ls = 0.f, a0 = 0.f, a1 = 0.f;
+  float M = -INFINITY, Ls = 0.f;
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < nsplit; c0 += CH) {
     const int nc = min(CH, nsplit - c0);
-    // (m, l) of split c0 + lane, loaded unconditionally from a clamped split
+    // (m, l) of split c0 + lane, and the o of splits c0 + 2t + hh, loaded
+    // unconditionally from clamped splits
     float2 ml = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(lane, nc - 1)) * kPart);
-    float2 ov[CH];
+    f4_t ov[CH / 2];
 #pragma unroll
-    for (int s = 0; s < CH; ++s)
-      ov[s] = *reinterpret_cast<const float2*>(pb + (int64_t)(c0 + min(s, nc - 1)) * kPart + 4 +
-                                               2 * lane);
+    for (int t = 0; t < CH / 2; ++t)
+      ov[t] = *reinterpret_cast<const f4_t*>(pb + (int64_t)(c0 + min(2 * t + hh, nc - 1)) * kPart +
+                                             4 + 4 * j);
     // Every load of the round precedes the first wait: the empty asm takes
-    // every loaded register.  Left to itself the compiler issued ~18 of the
-    // 34 loads, waited for (m, l), ran the max / exp and only then issued
-    // the rest (two memory round trips); a load under `lane < nc` was waited
-    // for on its own.  A memory clobber would not order these loads (the
-    // partials are read-only and restrict-qualified).
+    // every loaded register (a memory clobber would not order these loads:
+    // the partials are read-only and restrict-qualified).
     asm volatile("" : "+v"(ml.x), "+v"(ml.y));
 #pragma unroll
-    for (int s = 0; s < CH; ++s) asm volatile("" : "+v"(ov[s].x), "+v"(ov[s].y));
+    for (int t = 0; t < CH / 2; ++t)
+      asm volatile("" : "+v"(ov[t][0]), "+v"(ov[t][1]), "+v"(ov[t][2]), "+v"(ov[t][3]));
     const float ms = lane < nc ? ml.x : -INFINITY, ls = lane < nc ? ml.y : 0.f;
     const float Mn = fmaxf(M, wave_max(ms));
-    const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);  // rescale of earlier chunks
+    const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);  // rescale of earlier rounds
     const float w = (ms == -INFINITY) ? 0.f : __expf(ms - Mn);
     Ls = __builtin_fmaf(Ls, r, wave_sum(w * ls));
-    a0 *= r;
-    a1 *= r;
+    acc *= r;
 #pragma unroll
-    for (int s = 0; s < CH; ++s) {
-      const float ws = readlane_f(w, s);  // 0 past the chunk end
-      a0 = __builtin_fmaf(ws, ov[s].x, a0);
-      a1 = __builtin_fmaf(ws, ov[s].y, a1);
+    for (int t = 0; t < CH / 2; ++t) {
+      const float we = readlane_f(w, 2 * t), wo = readlane_f(w, 2 * t + 1);  // 0 past the end
+      const float ws = hh ? wo : we;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(ws, ov[t][k], acc[k]);
     }
     M = Mn;
   }
-  const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-  *reinterpret_cast<uint32_t*>(outp + b * out_stride + (int64_t)h * 128 + 2 * lane) =
-      (uint32_t)f2h(a0 * inv) | ((uint32_t)f2h(a1 * inv) << 16);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) acc[k] += __shfl_xor(acc[k], 32);  // even + odd splits
+  if (hh == 0) {
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+    const uint32_t lo = (uint32_t)f2h(acc[0] * inv) | ((uint32_t)f2h(acc[1] * inv) << 16);
+    const uint32_t hi = (uint32_t)f2h(acc[2] * inv) | ((uint32_t)f2h(acc[3] * inv) << 16);
+    *reinterpret_cast<u2_t*>(outp + b * out_stride + (int64_t)h * 128 + 4 * j) = u2_t{lo, hi};
+  }
 }
 
 }  // namespace
