@@ -116,9 +116,11 @@ R4Q_API int r4q_gemm(const void* x, const void* w, const void* sz, void* y,
  * the K units of the remaining tiles are shared evenly by the CUs
  * (stream-K; none when the tiles fill their rounds to 7/8 or more; with at
  * most 128 tiles each tile is split into floor(256 / tiles) equal pieces),
- * for 2 <= M <= 16 the weight tiles split along K.  Split tiles keep fp32 partials in the
- * workspace, summed in a fixed order (deterministic for a given shape and
- * workspace size; within fp32 rounding of the unsplit product).  Same role
+ * for 2 <= M <= 16 the weight tiles split along K.  Split tiles keep partials
+ * in the workspace (M >= 256: fp16 per segment; M <= 16: fp32), summed in
+ * fp32 in a fixed order (deterministic for a given shape and workspace
+ * size; M >= 256 within fp16 rounding of each segment of the unsplit
+ * product).  Same role
  * as the rocBLAS workspace behind the reference's at::mm_out in
  * dequant_matmul_out (hip:1973-1988). */
 R4Q_API int r4q_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int wbits,

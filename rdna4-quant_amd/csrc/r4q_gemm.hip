@@ -276,9 +276,10 @@ __device__ __forceinline__ h8_t skinny_b(const u4_t w, uint32_t s2, int d) {
 // [floor(w * TU / sk), floor((w + 1) * TU / sk)) (TU = (T - dp) * U), i.e. the
 // tail of one tile, whole tiles, the head of another.  A tile done by one
 // workgroup is written as fp16 directly; a tile shared by several writes one
-// fp32 partial per workgroup (segment j = w - the first workgroup on the
-// tile) and gemm_splitk_reduce_kernel sums them in segment order, so the
-// result does not depend on timing.
+// fp16 partial per workgroup (segment j = w - the first workgroup on the
+// tile; fp16 halves the partial traffic, written and read back, at one
+// extra rounding of each segment's sum) and gemm_splitk_reduce_kernel sums
+// them in fp32 in segment order, so the result does not depend on timing.
 constexpr int RBM = 256, RBN = 256, RBK = 32;
 constexpr int kRingWaves = 4;  // one per SIMD; wave w owns output columns 64w .. 64w+63
 constexpr int kRingThreads = 64 * kRingWaves;
@@ -667,7 +668,7 @@ struct RingSeg {
 template <int WBITS>
 __global__ __launch_bounds__(kRingThreads, 1) void gemm_ring_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, float* __restrict__ part, int M,
+    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, uint16_t* __restrict__ part, int M,
     int N, int K, int dp, int sk, int U, int maxseg) {
   using R = Ring<WBITS>;
   __shared__ __align__(16) uint8_t ring[R::kBytes];
@@ -750,17 +751,22 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemm_ring_kernel(
     int tq = t;
     asm volatile("" : "+v"(tq));
     if (!whole) {
-      // fp32 partial in the accumulator layout: float4 of (wave, i8, j, lane)
-      // at ((wave * 16 + i8) * 4 + j) * 64 + lane (16-byte stores, 1 KB per
-      // wave instruction); gemm_splitk_reduce_kernel reads the same layout
+      // fp16 partial in the accumulator layout: the 8 values of N-blocks
+      // 2 jp and 2 jp + 1 of (wave, i8, lane) as one 16-byte piece at
+      // ((wave * 16 + i8) * 2 + jp) * 64 + lane (1 KB per wave
+      // instruction); gemm_splitk_reduce_kernel reads the same layout
       const int tl = ctile - dp;
       const int j = w - sk_owner((int64_t)tl * U, TU, sk);
-      f4_t* pt = reinterpret_cast<f4_t*>(part + ((int64_t)tl * maxseg + j) * (RBM * RBN));
-      pt += (tq >> 6) * (16 * 4 * 64) + (tq & 63);
+      u4_t* pt = reinterpret_cast<u4_t*>(part + ((int64_t)tl * maxseg + j) * (RBM * RBN));
+      pt += (tq >> 6) * (16 * 2 * 64) + (tq & 63);
 #pragma unroll
       for (int i8 = 0; i8 < 16; ++i8)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) pt[(i8 * 4 + jj) * 64] = acc[i8][jj];
+        for (int jp = 0; jp < 2; ++jp) {
+          const f4_t a = acc[i8][2 * jp], c = acc[i8][2 * jp + 1];
+          pt[(i8 * 2 + jp) * 64] = u4_t{cvt_pk_h(a[0], a[1]), cvt_pk_h(a[2], a[3]),
+                                        cvt_pk_h(c[0], c[1]), cvt_pk_h(c[2], c[3])};
+        }
     } else {
       // C fragment: lane holds rows 4g + r of an M-block, column c of an N-block
       const int ec = tq & 15, eg = (tq >> 4) & 3, ewn = (tq >> 6) * 64;
@@ -779,20 +785,21 @@ __global__ __launch_bounds__(kRingThreads, 1) void gemm_ring_kernel(
   }
 }
 
-// Y = fp16(sum over the segments of each shared tile, in segment order).
-// Partials are in the accumulator layout of gemm_ring_kernel (float4 of
-// (wave, i8, j, lane)); a thread takes lanes 16g + 4q .. + 3 of one
-// (wave, i8, j) -- 64 contiguous bytes, rows 16 i8 + 4g .. + 3 x columns
-// 64 wave + 16 j + 4q .. + 3 of the tile -- and writes 4 x 4 outputs.  The
-// loads of up to 8 segments are in flight before they are added in order.
-constexpr int kRedThreadsPerTile = RBM * RBN / 16;
-__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
+// Y = fp16(sum over the segments of each shared tile, in segment order, in
+// fp32).  Partials are fp16 in the accumulator layout of gemm_ring_kernel
+// (16-byte pieces of (wave, i8, jp, lane): N-blocks 2 jp and 2 jp + 1 of a
+// lane); a thread takes lanes 16g + 4q .. + 3 of one (wave, i8, jp) -- 64
+// contiguous bytes, rows 16 i8 + 4g .. + 3 x columns 64 wave + 16 j + 4q ..
+// + 3 for j = 2 jp, 2 jp + 1 -- and writes 4 x 8 outputs.  The loads of up
+// to 4 segments are in flight before they are added in order.
+constexpr int kRedThreadsPerTile = RBM * RBN / 32;
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const uint16_t* __restrict__ part,
                                                                  uint16_t* __restrict__ Y, int M,
                                                                  int N, int dp, int sk, int U,
                                                                  int maxseg) {
   const int gt = blockIdx.x * 256 + threadIdx.x;
   const int tl = gt / kRedThreadsPerTile, x = gt % kRedThreadsPerTile;
-  const int q = x & 3, g = (x >> 2) & 3, j = (x >> 4) & 3, i8 = (x >> 6) & 15, wv = x >> 10;
+  const int q = x & 3, g = (x >> 2) & 3, jp = (x >> 4) & 1, i8 = (x >> 5) & 15, wv = x >> 9;
   const int ntn = (N + RBN - 1) / RBN;
   const int tiles = ntn * ((M + RBM - 1) / RBM);
   const int64_t TU = (int64_t)(tiles - dp) * U;
@@ -801,41 +808,61 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __
   if (w1 == w0) return;  // written whole by one workgroup
   const int tile = dp + tl;
   const int row0 = (tile / ntn) * RBM + 16 * i8 + 4 * g;
-  const int col0 = (tile % ntn) * RBN + 64 * wv + 16 * j + 4 * q;
-  if (row0 >= M || col0 >= N) return;
+  const int colb = (tile % ntn) * RBN + 64 * wv + 32 * jp + 4 * q;  // N-block 2 jp
+  if (row0 >= M || colb >= N) return;
   const int nseg = w1 - w0 + 1;
-  const f4_t* p = reinterpret_cast<const f4_t*>(part + (int64_t)tl * maxseg * (RBM * RBN)) +
-                  ((wv * 16 + i8) * 4 + j) * 64 + 16 * g + 4 * q;
-  constexpr int64_t kSeg = RBM * RBN / 4;  // float4 per segment
-  f4_t v[4];
+  const u4_t* p = reinterpret_cast<const u4_t*>(part + (int64_t)tl * maxseg * (RBM * RBN)) +
+                  ((wv * 16 + i8) * 2 + jp) * 64 + 16 * g + 4 * q;
+  constexpr int64_t kSeg = RBM * RBN / 8;  // 16-byte pieces per segment
+  // v[b][l][r]: N-block 2 jp + b, column 4q + l, row 4g + r
+  float v[2][4][4];
+  auto add = [&](const u4_t (&t)[4], bool first) {
 #pragma unroll
-  for (int l = 0; l < 4; ++l) v[l] = p[l];
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t wd = t[l][2 * b + h];
+          const float lo = h2f((uint16_t)(wd & 0xFFFFu)), hi = h2f((uint16_t)(wd >> 16));
+          v[b][l][2 * h] = first ? lo : v[b][l][2 * h] + lo;
+          v[b][l][2 * h + 1] = first ? hi : v[b][l][2 * h + 1] + hi;
+        }
+  };
+  {
+    u4_t t[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) t[l] = p[l];
+    add(t, true);
+  }
   for (int j0 = 1; j0 < nseg; j0 += 4) {
-    f4_t t[4][4];
+    u4_t t[4][4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int l = 0; l < 4; ++l) t[s][l] = p[(int64_t)min(j0 + s, nseg - 1) * kSeg + l];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      if (j0 + s < nseg)
-#pragma unroll
-        for (int l = 0; l < 4; ++l) v[l] += t[s][l];
+      if (j0 + s < nseg) add(t[s], false);
   }
-  // v[l][r]: row row0 + r, column col0 + l
-  const bool vec = col0 + 4 <= N && (N & 3) == 0;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    if (row0 + r >= M) break;
-    uint16_t* y = Y + (int64_t)(row0 + r) * N + col0;
-    if (vec) {
-      const uint32_t lo = (uint32_t)f2h(v[0][r]) | ((uint32_t)f2h(v[1][r]) << 16);
-      const uint32_t hi = (uint32_t)f2h(v[2][r]) | ((uint32_t)f2h(v[3][r]) << 16);
-      *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
-    } else {
+  for (int b = 0; b < 2; ++b) {
+    const int col0 = colb + 16 * b;
+    if (col0 >= N) break;
+    const bool vec = col0 + 4 <= N && (N & 3) == 0;
 #pragma unroll
-      for (int l = 0; l < 4; ++l)
-        if (col0 + l < N) y[l] = f2h(v[l][r]);
+    for (int r = 0; r < 4; ++r) {
+      if (row0 + r >= M) break;
+      uint16_t* y = Y + (int64_t)(row0 + r) * N + col0;
+      if (vec) {
+        const uint32_t lo = (uint32_t)f2h(v[b][0][r]) | ((uint32_t)f2h(v[b][1][r]) << 16);
+        const uint32_t hi = (uint32_t)f2h(v[b][2][r]) | ((uint32_t)f2h(v[b][3][r]) << 16);
+        *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
+      } else {
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+          if (col0 + l < N) y[l] = f2h(v[b][l][r]);
+      }
     }
   }
 }
@@ -1327,7 +1354,7 @@ bool gemm_ring_ok(int64_t M, int64_t N, int64_t K, int wbits) {
 // then sk stream-K workgroups over the other tiles.
 struct RingPlan {
   int dp = 0, sk = 0, U = 1, maxseg = 1;
-  size_t ws = 0;  // fp32 partials: (tiles - dp) * maxseg * 256 * 256 * 4 bytes
+  size_t ws = 0;  // fp16 partials: (tiles - dp) * maxseg * 256 * 256 * 2 bytes
 };
 
 constexpr int kRingCUs = 256;  // MI355X compute units: one ring workgroup each (LDS-bound)
@@ -1382,7 +1409,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
     for (int64_t t = 0; t < tiles - dp; ++t)
       maxseg = std::max(maxseg, host_sk_owner(t * pl.U + pl.U - 1, TU, sk) -
                                     host_sk_owner(t * pl.U, TU, sk) + 1);
-    const size_t ws = maxseg > 1 ? (size_t)(tiles - dp) * maxseg * RBM * RBN * 4 : 0;
+    const size_t ws = maxseg > 1 ? (size_t)(tiles - dp) * maxseg * RBM * RBN * 2 : 0;
     if (ws <= ws_bytes) {
       pl.dp = (int)dp;
       pl.sk = (int)sk;
@@ -1411,7 +1438,7 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
   auto* yp = static_cast<uint16_t*>(y);
   if (gemm_ring_ok(M, N, K, wbits)) {
     const RingPlan pl = ring_plan(M, N, K, wbits, ws ? ws_bytes : 0);
-    float* part = pl.ws ? static_cast<float*>(ws) : nullptr;
+    uint16_t* part = pl.ws ? static_cast<uint16_t*>(ws) : nullptr;
     const unsigned blocks = (unsigned)(pl.dp + pl.sk);
     if (wbits == 4)
       hipLaunchKernelGGL(gemm_ring_kernel<4>, dim3(blocks), dim3(kRingThreads), 0, st, xp, wp, sp,
