@@ -356,9 +356,10 @@ __device__ __forceinline__ void stage_x_norm(const NormIn& in, const GemvNorm& n
 // scaling and rounding of silu_kernel<true> (fwht32, store32h), so the
 // staged activation is bit-identical to that kernel's output.  Thread t
 // stages pieces t, t + 256, ... (at most NPF); all of them are requested
-// before the first weight steps (see NormIn): each as 32 dwords, from h
-// for an fp32 piece or from x (its 16 dwords read twice) for an fp16 one,
-// at clamped addresses and without branches.
+// before the first weight steps (see NormIn), at clamped addresses: a round
+// of 256 pieces wholly below the split as 16 dwords of x each, any other as
+// 32 dwords, from h for an fp32 piece or from x (its 16 dwords read twice)
+// for an fp16 one, without per-thread branches.
 template <int WBITS, int LPR, int CPL>
 struct FwhtIn {
   static constexpr int XD = Fmt<WBITS>::kXDw;
@@ -376,16 +377,32 @@ __device__ __forceinline__ void fwht_issue(const uint16_t* __restrict__ x,
 #pragma unroll
   for (int i = 0; i < FwhtIn<WBITS, LPR, CPL>::NPF; ++i) {
     const int p = min((int)threadIdx.x + 256 * i, K / 32 - 1);
-    const bool half = 32 * p < split;
-    const u4_t* src = half ? reinterpret_cast<const u4_t*>(x + (int64_t)p * 32)
-                           : reinterpret_cast<const u4_t*>(h + (int64_t)p * 32);
+    if (256 * i + 256 <= split / 32) {
+      // the whole round is fp16 (workgroup-uniform; the SiLU split puts
+      // whole rounds of 256 pieces below it): 16 dwords per piece
+      const u4_t* src = reinterpret_cast<const u4_t*>(x + (int64_t)p * 32);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const u4_t v = src[half ? (q & 3) : q];
-      in.raw[i][4 * q] = v[0];
-      in.raw[i][4 * q + 1] = v[1];
-      in.raw[i][4 * q + 2] = v[2];
-      in.raw[i][4 * q + 3] = v[3];
+      for (int q = 0; q < 4; ++q) {
+        const u4_t v = src[q];
+        in.raw[i][4 * q] = v[0];
+        in.raw[i][4 * q + 1] = v[1];
+        in.raw[i][4 * q + 2] = v[2];
+        in.raw[i][4 * q + 3] = v[3];
+      }
+#pragma unroll
+      for (int k = 16; k < 32; ++k) in.raw[i][k] = 0u;  // unused by fp16 pieces
+    } else {
+      const bool half = 32 * p < split;
+      const u4_t* src = half ? reinterpret_cast<const u4_t*>(x + (int64_t)p * 32)
+                             : reinterpret_cast<const u4_t*>(h + (int64_t)p * 32);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const u4_t v = src[half ? (q & 3) : q];
+        in.raw[i][4 * q] = v[0];
+        in.raw[i][4 * q + 1] = v[1];
+        in.raw[i][4 * q + 2] = v[2];
+        in.raw[i][4 * q + 3] = v[3];
+      }
     }
   }
 }
