@@ -374,10 +374,16 @@ template <int WBITS, int LPR, int CPL>
 __device__ __forceinline__ void fwht_issue(const uint16_t* __restrict__ x,
                                            const float* __restrict__ h, int split,
                                            FwhtIn<WBITS, LPR, CPL>& in, int K) {
+  const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
 #pragma unroll
   for (int i = 0; i < FwhtIn<WBITS, LPR, CPL>::NPF; ++i) {
     const int p = min((int)threadIdx.x + 256 * i, K / 32 - 1);
-    if (256 * i + 256 <= split / 32) {
+    if (i > 0 && 256 * i + 64 * wv >= K / 32) {
+      // wave-uniform: no piece of this wave in this round (none staged), and
+      // the wave has loads of earlier rounds in flight on either path
+#pragma unroll
+      for (int k = 0; k < 32; ++k) in.raw[i][k] = 0u;
+    } else if (256 * i + 256 <= split / 32) {
       // the whole round is fp16 (workgroup-uniform; the SiLU split puts
       // whole rounds of 256 pieces below it): 16 dwords per piece
       const u4_t* src = reinterpret_cast<const u4_t*>(x + (int64_t)p * 32);
