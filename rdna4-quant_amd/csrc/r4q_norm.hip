@@ -64,55 +64,65 @@ __global__ __launch_bounds__(1024) void rownorm_kernel(const uint16_t* __restric
 // rownorm_kernel<3> (residual + RMSNorm + FWHT-32) whose input a is the
 // split-K sum of a projection, a = fp16(sum over s < S of ap[s * plane +
 // row * D + i]) in split order -- the arithmetic of gemm_skinny_reduce_kernel
-// -- so the outputs equal that reduce followed by rownorm_kernel<3>.  The S
-// planes are read coalesced by the whole workgroup while the thread's
-// residual and weight chunks are in flight, and the fp16 row is staged in
-// LDS; then one thread per 32-chunk as in rownorm_kernel (the threads past
-// the chunks add exact zeros to the sum of squares).  KF float4 per thread
-// per plane: D <= 4 * KF * kPsumThreads.
-constexpr int kPsumThreads = 512;
+// -- so the outputs equal that reduce followed by rownorm_kernel<3>.  One
+// workgroup per row, its waves in two roles, so that every load instruction
+// carries a full wave of useful bytes (the kernel is bound by the rate at
+// which its loads issue, not by their bytes):
+//  * the first 5/8 of the threads (PT) read the S planes coalesced (KF
+//    float4 per thread and plane), add them in split order and stage the
+//    fp16 row in LDS;
+//  * the other CT threads, one per 32-element chunk, load their residual
+//    and weight chunks meanwhile, then run the chunk norm as rownorm_kernel
+//    does from the staged row (the sum of squares over the waves in order:
+//    the plane waves add exact zeros).
+// D <= 4 KF PT and D / 32 <= CT.
 constexpr int kPsumMaxS = 4;
-template <int KF>
-__global__ __launch_bounds__(kPsumThreads) void rownorm_psum_kernel(
-    const float* __restrict__ ap, int64_t plane, int S, const uint16_t* __restrict__ b,
+template <int NT, int KF, int S>
+__global__ __launch_bounds__(NT) void rownorm_psum_kernel(
+    const float* __restrict__ ap, int64_t plane, const uint16_t* __restrict__ b,
     const uint16_t* __restrict__ w, uint16_t* __restrict__ y, uint16_t* __restrict__ res_out,
     int D, float eps) {
-  __shared__ float red[16];
-  __shared__ __align__(16) uint32_t as[2 * KF * kPsumThreads];  // the fp16 row
+  constexpr int PT = NT / 8 * 5;  // plane threads (whole waves)
+  __shared__ float red[NT / 64];
+  __shared__ __align__(16) uint32_t as[2 * KF * PT];  // the fp16 row
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, nch = D / 32, nf = D / 4;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   typedef float f4v __attribute__((ext_vector_type(4)));
-  f4v v[KF][kPsumMaxS];
-  const float* pr = ap + row * D;
-#pragma unroll
-  for (int k = 0; k < KF; ++k) {
-    const int f = min(t + k * kPsumThreads, nf - 1);  // clamped, unused past nf
-#pragma unroll
-    for (int z = 0; z < kPsumMaxS; ++z)
-      v[k][z] = *reinterpret_cast<const f4v*>(pr + min(z, S - 1) * plane + 4 * f);
-  }
   uint32_t bv[16], g[16];
-  const int c = min(t, nch - 1);
-  load16w(b + row * D + c * 32, bv);
-  load16w(w + c * 32, g);
+  if (wv < PT / 64) {
+    const float* pr = ap + row * D;
+    f4v v[KF][S];
 #pragma unroll
-  for (int k = 0; k < KF; ++k) {
-    const int f = t + k * kPsumThreads;
-    if (f < nf) {
-      f4v a = v[k][0];
+    for (int k = 0; k < KF; ++k) {
+      const int f = min(t + k * PT, nf - 1);  // clamped, unused past nf
 #pragma unroll
-      for (int z = 1; z < kPsumMaxS; ++z)
-        if (z < S) a += v[k][z];
-      as[2 * f] = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
-      as[2 * f + 1] = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
+      for (int z = 0; z < S; ++z) v[k][z] = *reinterpret_cast<const f4v*>(pr + z * plane + 4 * f);
     }
+#pragma unroll
+    for (int k = 0; k < KF; ++k) {
+      const int f = t + k * PT;
+      if (f < nf) {
+        f4v a = v[k][0];
+#pragma unroll
+        for (int z = 1; z < S; ++z) a += v[k][z];
+        as[2 * f] = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
+        as[2 * f + 1] = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
+      }
+    }
+  } else {
+    const int c = min(t - PT, nch - 1);
+    load16w(b + row * D + c * 32, bv);
+    load16w(w + c * 32, g);
   }
   __syncthreads();
+  const int c = t - PT;
+  const bool act = c >= 0 && c < nch;
   uint32_t r[16];
   float ss = 0.f;
-  if (t < nch) {
+  if (act) {
     uint32_t av[16];
-    const u4_t* s4 = reinterpret_cast<const u4_t*>(as + 16 * t);
+    const u4_t* s4 = reinterpret_cast<const u4_t*>(as + 16 * c);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const u4_t d = s4[i];
@@ -125,11 +135,11 @@ __global__ __launch_bounds__(kPsumThreads) void rownorm_psum_kernel(
   }
   const float tot = block_sum(ss, red);
   const float rrms = 1.0f / __builtin_sqrtf(tot / (float)D + eps);
-  if (t < nch) {
+  if (act) {
     uint32_t o[16];
-    store16w(res_out + row * D + t * 32, r);
+    store16w(res_out + row * D + c * 32, r);
     norm_chunk_scale<true>(r, g, rrms, o);
-    store16w(y + row * D + t * 32, o);
+    store16w(y + row * D + c * 32, o);
   }
 }
 
@@ -286,8 +296,12 @@ int launch_rownorm(int mode, const void* a, const void* b, const void* w, void* 
   }
 }
 
+// Threads per rownorm_psum workgroup: 512 up to D = 5120 (4 float4 per plane
+// thread, 192 chunk threads), 1024 up to D = 10240.
+int psum_threads(int64_t D) { return D <= 5120 ? 512 : 1024; }
+
 bool rownorm_psum_ok(int64_t D, int S) {
-  return D % 32 == 0 && D > 0 && D <= 4 * 4 * kPsumThreads && S >= 2 && S <= kPsumMaxS;
+  return D % 32 == 0 && D > 0 && D <= 10240 && S >= 2 && S <= kPsumMaxS;
 }
 
 int launch_rownorm_psum(const float* ap, int64_t plane, int S, const void* b, const void* w,
@@ -299,18 +313,33 @@ int launch_rownorm_psum(const float* ap, int64_t plane, int S, const void* b, co
   R4Q_REQUIRE(plane >= rows * D && al16(ap) && al16(b) && al16(w) && al16(y) && al16(res_out),
               "res_rmsnorm_fwht (split sum): bad plane or alignment");
   if (rows == 0) return R4Q_OK;
-  const int kf = (int)((D / 4 + kPsumThreads - 1) / kPsumThreads);
-#define R4Q_PSUM(KF)                                                                            \
-  hipLaunchKernelGGL((rownorm_psum_kernel<KF>), dim3((unsigned)rows), dim3(kPsumThreads), 0, st, \
-                     ap, plane, S, static_cast<const uint16_t*>(b),                             \
-                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y),                \
+  const int nt = psum_threads(D), pt = nt / 8 * 5;
+  const int kf = (int)((D / 4 + pt - 1) / pt);
+#define R4Q_PSUM(NT, KF, SS)                                                                   \
+  hipLaunchKernelGGL((rownorm_psum_kernel<NT, KF, SS>), dim3((unsigned)rows), dim3(NT), 0, st, \
+                     ap, plane, static_cast<const uint16_t*>(b),                               \
+                     static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y),               \
                      static_cast<uint16_t*>(res_out), (int)D, eps)
-  switch (kf) {
-    case 1: R4Q_PSUM(1); break;
-    case 2: R4Q_PSUM(2); break;
-    case 3: R4Q_PSUM(3); break;
-    default: R4Q_PSUM(4);
+#define R4Q_PSUM_S(NT, KF)            \
+  switch (S) {                        \
+    case 2: R4Q_PSUM(NT, KF, 2); break; \
+    case 3: R4Q_PSUM(NT, KF, 3); break; \
+    default: R4Q_PSUM(NT, KF, 4);       \
   }
+#define R4Q_PSUM_K(NT)                \
+  switch (kf) {                       \
+    case 1: R4Q_PSUM_S(NT, 1); break; \
+    case 2: R4Q_PSUM_S(NT, 2); break; \
+    case 3: R4Q_PSUM_S(NT, 3); break; \
+    default: R4Q_PSUM_S(NT, 4);       \
+  }
+  if (nt == 512) {
+    R4Q_PSUM_K(512)
+  } else {
+    R4Q_PSUM_K(1024)
+  }
+#undef R4Q_PSUM_K
+#undef R4Q_PSUM_S
 #undef R4Q_PSUM
   return launch_status("res_rmsnorm_fwht (split sum)");
 }
