@@ -84,7 +84,9 @@ __device__ __forceinline__ f4_t mfma16(u4_t a, u4_t b, f4_t c) {
 // the codes into its own (earlier issued) loads.  Epilogue: FWHT-32 per
 // 32-dim chunk, then the fp32 partial (m, l, o) or, with one split, the
 // normalised fp16 output.
-template <int G, bool NORMQ>
+// QS (NORMQ only): 0 = raw fp16 QKV rows, 2..kMaxQkvSplits = that many fp32
+// split planes of the qkv projection to sum (exactly QS loads per element).
+template <int G, bool NORMQ, int QS = 0>
 __global__ __launch_bounds__(256) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, int64_t q_stride, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const float* __restrict__ ksc, const float* __restrict__ vsc,
@@ -163,7 +165,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
   const bool owner = NORMQ && (pos >> 5) % nsplit == sp;  // holds the new position's chunk
   const int ntask = G + (owner ? 2 : 0);
   uint16_t px[kSlots][2], pw[kSlots][2];  // raw fp16, widened after the KV loads issue
-  float pf[NORMQ ? kSlots : 1][2][kMaxQkvSplits];  // split partials (qk.nsum >= 2)
+  static_assert(QS == 0 || (NORMQ && QS >= 2 && QS <= kMaxQkvSplits), "split planes to sum");
+  float pf[NORMQ && QS >= 2 ? kSlots : 1][2][QS >= 2 ? QS : 1];  // split partials
   uint16_t pc = 0, ps = 0;
   if constexpr (NORMQ) {
     // branch-free, so that all of them are in flight together (slots past
@@ -173,10 +176,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
       const int task = wave + 4 * i;
       const int head = task >= ntask ? 0 : task < G ? kh * G + task : task == G ? H + kh : H + Hk + kh;
       const int64_t off = b * q_stride + (int64_t)head * 128;  // raw QKV row: q | k | v heads
-      if (qk.nsum >= 2) {  // wave-uniform
+      if constexpr (QS >= 2) {
 #pragma unroll
-        for (int z = 0; z < kMaxQkvSplits; ++z) {
-          const float* src = qk.part + min(z, qk.nsum - 1) * qk.plane + off;
+        for (int z = 0; z < QS; ++z) {
+          const float* src = qk.part + z * qk.plane + off;
           pf[i][0][z] = src[lane];
           pf[i][1][z] = src[lane + 64];
         }
@@ -207,15 +210,14 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     // widened in straight-line code: every slot's loads are consumed here,
     // before any branch (none is sunk behind the KV loads)
     const float c = h2f_ieee(pc), sn = h2f_ieee(ps);
-    if (qk.nsum >= 2) {  // the split reduce's sum, in split order, rounded to fp16
+    if constexpr (QS >= 2) {  // the split reduce's sum, in split order, rounded to fp16
 #pragma unroll
       for (int i = 0; i < kSlots; ++i)
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           float v = pf[i][e][0];
 #pragma unroll
-          for (int z = 1; z < kMaxQkvSplits; ++z)
-            if (z < qk.nsum) v += pf[i][e][z];
+          for (int z = 1; z < QS; ++z) v += pf[i][e][z];
           px[i][e] = f2h(v);
         }
     }
@@ -584,20 +586,28 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   if (nsplit < 1 || nsplit > kMaxSplits)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: %d splits outside [1, %d]", nsplit, kMaxSplits);
   if (nsplit > 1 && !ws) return fail(R4Q_EINVAL, "flash_decode: no split workspace");
+  if (qk && qk->nsum > kMaxQkvSplits)
+    return fail(R4Q_EUNSUPPORTED, "flash_decode: %d qkv split planes (at most %d)", qk->nsum,
+                kMaxQkvSplits);
   const dim3 grid((unsigned)nsplit, (unsigned)Hk, (unsigned)B);
   float* part = ws;
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
   const auto* vp = static_cast<const uint8_t*>(v_cache);
   bool launched = false;
+#define R4Q_ATTN_QK(GG, QQ)                                                                   \
+  hipLaunchKernelGGL((attn_mfma_kernel<GG, true, QQ>), grid, dim3(256), 0, st, qp, q_stride,   \
+                     kp, vp, k_scale, v_scale, part, static_cast<uint16_t*>(out), out_stride,  \
+                     fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len, seq_len_dev, nsplit,  \
+                     *qk)
 #define R4Q_ATTN_MFMA(GG)                                                                     \
   if (!launched && G == GG) {                                                                 \
-    if (qk)                                                                                   \
-      hipLaunchKernelGGL((attn_mfma_kernel<GG, true>), grid, dim3(256), 0, st, qp, q_stride,   \
-                         kp, vp, k_scale, v_scale, part, static_cast<uint16_t*>(out),         \
-                         out_stride, fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len,       \
-                         seq_len_dev, nsplit, *qk);                                           \
-    else                                                                                      \
+    if (qk) {                                                                                 \
+      if (qk->nsum < 2) R4Q_ATTN_QK(GG, 0);                                                   \
+      else if (qk->nsum == 2) R4Q_ATTN_QK(GG, 2);                                             \
+      else if (qk->nsum == 3) R4Q_ATTN_QK(GG, 3);                                             \
+      else R4Q_ATTN_QK(GG, 4);                                                                \
+    } else                                                                                    \
       hipLaunchKernelGGL((attn_mfma_kernel<GG, false>), grid, dim3(256), 0, st, qp, q_stride,  \
                          kp, vp, k_scale, v_scale, part, static_cast<uint16_t*>(out),         \
                          out_stride, fwht, (int)H, (int)Hk, (int)max_seq, (int)seq_len,       \
@@ -606,6 +616,7 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   }
   R4Q_ATTN_MFMA(1) R4Q_ATTN_MFMA(2) R4Q_ATTN_MFMA(4) R4Q_ATTN_MFMA(5) R4Q_ATTN_MFMA(8)
 #undef R4Q_ATTN_MFMA
+#undef R4Q_ATTN_QK
   if (!launched)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
   if (nsplit > 1) {
