@@ -499,10 +499,10 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 //   m* = max_s m_s,  out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s.
 // The two half-waves take the even and the odd splits, lane j of a half
 // owning dims 4j .. 4j+3 (16-byte loads: one instruction reads two splits'
-// o), and add their sums at the end.  CH splits per round (16, 32 or 64:
-// the smallest covering the split count) with a running maximum; every load
-// of a round is issued before any arithmetic; slots past the last split
-// re-read it and get weight 0, so CH does not change the result.
+// o), and add their sums at the end.  CH splits per round (16, 18, 24, 32
+// or 64: the smallest covering the split count) with a running maximum;
+// every load of a round is issued before any arithmetic; slots past the
+// last split re-read it and get weight 0, so CH does not change the result.
 template <int CH>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part,
                                                         uint16_t* __restrict__ outp,
@@ -624,6 +624,12 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
     auto* o16 = static_cast<uint16_t*>(out);
     if (nsplit <= 16)
       hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         nsplit);
+    else if (nsplit <= 18)
+      hipLaunchKernelGGL(attn_merge_kernel<18>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         nsplit);
+    else if (nsplit <= 24)
+      hipLaunchKernelGGL(attn_merge_kernel<24>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
                          nsplit);
     else if (nsplit <= 32)
       hipLaunchKernelGGL(attn_merge_kernel<32>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
