@@ -29,6 +29,7 @@ namespace {
 
 constexpr int kMaxSplits = 128;  // partials per (sequence, head)
 constexpr int kPart = 132;       // floats per (seq, head, split): m, l, pad, pad, o[128]
+constexpr int kXcds = 8;         // workgroup i is dispatched to XCD i % 8
 
 // ------------------------------------------------ MFMA flash-decode partials
 // E4M3 bytes 0-1 (HI: 2-3) of w -> fp16 pair, v_cvt_scalef32_pk_f16_fp8 with
@@ -93,8 +94,17 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
     float* __restrict__ part, uint16_t* __restrict__ outp, int64_t out_stride, int fwht, int H,
     int Hk, int max_seq, int L_host, const int* __restrict__ L_dev, int nsplit, AttnQK qk) {
   static_assert(G >= 1 && G <= 16, "query heads per KV head must fit 16 MFMA columns");
-  const int sp = blockIdx.x, kh = blockIdx.y;
-  const int64_t b = blockIdx.z;
+  // XCD-grouped order when the (sequence, KV head) pairs fill whole rounds
+  // of the 8 XCDs: the grid is (8 nsplit, pairs / 8), workgroups go to the
+  // XCDs round-robin in x-fastest order, so every split of pair p sits on
+  // XCD p % 8, where the pair's merge workgroups run too (measured 9 us
+  // faster per 40-layer step than splits spread over the XCDs); otherwise
+  // the grid is (nsplit, pairs)
+  const bool grouped = (int)gridDim.x != nsplit;
+  const int sp = grouped ? (int)blockIdx.x / kXcds : (int)blockIdx.x;
+  const int pair = grouped ? (int)blockIdx.y * kXcds + (int)blockIdx.x % kXcds : (int)blockIdx.y;
+  const int kh = pair % Hk;
+  const int64_t b = pair / Hk;
   const int L = L_dev ? *L_dev : L_host;
   // 32-position chunks are dealt to the splits round-robin (split sp takes
   // chunks sp, sp + nsplit, ...), so that at any moment the workgroups of a
@@ -506,10 +516,16 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 template <int CH>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part,
                                                         uint16_t* __restrict__ outp,
-                                                        int64_t out_stride, int H, int nsplit) {
+                                                        int64_t out_stride, int H, int G,
+                                                        int nsplit) {
   static_assert(CH % 2 == 0 && CH <= 64, "two splits per load, one (m, l) per lane");
-  const int h = blockIdx.x;
-  const int64_t b = blockIdx.y;
+  // on the XCD of the pair's partial workgroups (attn_mfma_kernel's order):
+  // grid (8 G, pairs / 8) or (G, pairs)
+  const bool grouped = (int)gridDim.x != G;
+  const int hq = grouped ? (int)blockIdx.x / kXcds : (int)blockIdx.x;
+  const int pair = grouped ? (int)blockIdx.y * kXcds + (int)blockIdx.x % kXcds : (int)blockIdx.y;
+  const int h = (pair % (H / G)) * G + hq;
+  const int64_t b = pair / (H / G);
   const int lane = threadIdx.x, hh = lane >> 5, j = lane & 31;
   const float* pb = part + (b * H + h) * (int64_t)nsplit * kPart;
   float M = -INFINITY, Ls = 0.f;
@@ -589,7 +605,10 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   if (qk && qk->nsum > kMaxQkvSplits)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: %d qkv split planes (at most %d)", qk->nsum,
                 kMaxQkvSplits);
-  const dim3 grid((unsigned)nsplit, (unsigned)Hk, (unsigned)B);
+  const int npair = (int)(B * Hk);  // (sequence, KV head) pairs
+  const bool grouped = npair % kXcds == 0;  // the kernels' XCD-grouped order
+  const dim3 grid(grouped ? (unsigned)(kXcds * nsplit) : (unsigned)nsplit,
+                  grouped ? (unsigned)(npair / kXcds) : (unsigned)npair);
   float* part = ws;
   const auto* qp = static_cast<const uint16_t*>(q);
   const auto* kp = static_cast<const uint8_t*>(k_cache);
@@ -620,23 +639,24 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
   if (!launched)
     return fail(R4Q_EUNSUPPORTED, "flash_decode: GQA ratio %d not built (1, 2, 4, 5, 8)", G);
   if (nsplit > 1) {
-    const dim3 mg((unsigned)H, (unsigned)B);
+    const dim3 mg(grouped ? (unsigned)(kXcds * G) : (unsigned)G,
+                  grouped ? (unsigned)(npair / kXcds) : (unsigned)npair);
     auto* o16 = static_cast<uint16_t*>(out);
     if (nsplit <= 16)
       hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
-                         nsplit);
+                         G, nsplit);
     else if (nsplit <= 18)
       hipLaunchKernelGGL(attn_merge_kernel<18>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
-                         nsplit);
+                         G, nsplit);
     else if (nsplit <= 24)
       hipLaunchKernelGGL(attn_merge_kernel<24>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
-                         nsplit);
+                         G, nsplit);
     else if (nsplit <= 32)
       hipLaunchKernelGGL(attn_merge_kernel<32>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
-                         nsplit);
+                         G, nsplit);
     else
       hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
-                         nsplit);
+                         G, nsplit);
   }
   return launch_status("flash_decode");
 }
