@@ -32,6 +32,7 @@ struct r4q_ctx {
   uint64_t buf_epoch = 0;
   r4q::DevBuf attn;      // flash-decode partials
   r4q::DevBuf step;      // decode-step activations
+  void* tail_zeroed = nullptr;  // batched gate/up tail counters known to be zero
   r4q::DevBuf prefill;   // prefill activations
   r4q::DevBuf misc;      // device-side position / counters
   r4q::DevBuf sample;    // sampling tables (kept zeroed between calls)

@@ -92,6 +92,7 @@ struct Bufs {
   uint16_t *h, *r, *rot, *qkv, *o, *gu, *y, *d, *logits;
   void* ws = nullptr;  // split-K partials of the batched projections
   size_t ws_bytes = 0;
+  void* tail = nullptr;  // batched gate/up: tail-piece counters + partials
   float* attn;
   int* state;
   int64_t* ids;
@@ -160,7 +161,24 @@ size_t step_gemm_ws(const r4q_model* m, const Dims& dm, int64_t B) {
   return gws;
 }
 
-int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsplit, Bufs& bf) {
+// Batched gate/up with the SiLU epilogue: workspace of its tail pieces (the
+// largest any layer's width asks for; 0 when no layer has a tail).
+size_t step_tail_ws(const r4q_model* m, const Dims& dm, int64_t B) {
+  size_t t = 0;
+  if (B > 1 && B <= 8)
+    for (int li = 0; li < dm.L; ++li) {
+      const int bits = m->layers[li].gu_bits;
+      if (bits != 16) t = std::max(t, skinny_silu_tail_bytes(dm.I, dm.D, bits));
+    }
+  return t;
+}
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsplit, hipStream_t st,
+            Bufs& bf) {
   const size_t D = dm.D, I = dm.I;
   const size_t lmN = m->final_norm ? (size_t)m->lm_N : 0;
   const size_t rotw = dm.qd > dm.D ? dm.qd : dm.D;
@@ -168,8 +186,9 @@ int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsp
                           B * I, B * D, B * lmN};
   size_t total = 0;
   for (size_t s : sizes) total += align256(s * 2);
-  const size_t gws = step_gemm_ws(m, dm, B);
-  R4Q_TRY(ctx->step.reserve(total + gws));
+  const size_t gws = step_gemm_ws(m, dm, B), tws = step_tail_ws(m, dm, B);
+  const void* old = ctx->step.ptr;
+  R4Q_TRY(ctx->step.reserve(total + align256(gws) + tws));
   uint16_t** dst[] = {&bf.h, &bf.r, &bf.rot, &bf.qkv, &bf.o, &bf.gu, &bf.y, &bf.d, &bf.logits};
   uint8_t* p = static_cast<uint8_t*>(ctx->step.ptr);
   for (int i = 0; i < 9; ++i) {
@@ -178,6 +197,16 @@ int reserve(r4q_ctx* ctx, const r4q_model* m, const Dims& dm, int64_t B, int nsp
   }
   bf.ws = gws ? p : nullptr;
   bf.ws_bytes = gws;
+  bf.tail = tws ? p + align256(gws) : nullptr;
+  // the tail counters start at zero and every launch leaves them at zero;
+  // a layout without them (another batch size) may have put other data there
+  if (bf.tail && (ctx->step.ptr != old || ctx->tail_zeroed != bf.tail)) {
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, st,
+                       static_cast<uint32_t*>(bf.tail),
+                       (int64_t)(skinny_silu_tail_cnt_bytes(dm.I) / 4));
+    R4Q_TRY(launch_status("decode workspace"));
+  }
+  ctx->tail_zeroed = bf.tail;
   R4Q_TRY(ctx->attn.reserve(attn_ws_bytes(B, dm.H, nsplit)));
   bf.attn = static_cast<float*>(ctx->attn.ptr);
   const size_t misc = align256(kStateWords * 4) + align256(B * 8) +
@@ -334,9 +363,14 @@ int enqueue_step(const r4q_model* m, const Dims& dm, int64_t B, int64_t pos_host
         const size_t gu_ws = silu_epilogue(B, I) ? 0 : bf.ws_bytes;
         if (gemm_skinny_silu_ok(B, I, D, y.gu_bits, gu_ws)) {
           // skinny GEMM with the SiLU gate + FWHT-32 in its epilogue
-          // (unsplit) or in its split reduce
-          R4Q_TRY(gemm_skinny_silu_launch(bf.rot, y.gu_w, y.gu_s, bf.y, B, I, D, y.gu_bits, st,
-                                          gu_ws ? bf.ws : nullptr, gu_ws));
+          // (unsplit, with its tail units cut into pieces over the CUs) or
+          // in its split reduce
+          if (gu_ws)
+            R4Q_TRY(gemm_skinny_silu_launch(bf.rot, y.gu_w, y.gu_s, bf.y, B, I, D, y.gu_bits, st,
+                                            bf.ws, gu_ws));
+          else
+            R4Q_TRY(gemm_skinny_silu_tail_launch(bf.rot, y.gu_w, y.gu_s, bf.y, B, I, D,
+                                                 y.gu_bits, st, bf.tail));
           gated = true;
         } else {
           R4Q_TRY(linear(bf.rot, y.gu_w, y.gu_s, bf.gu, B, 2 * I, D, y.gu_bits, st, bf));
@@ -721,8 +755,8 @@ int decode_step(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
   R4Q_REQUIRE(!logits || m->final_norm, "decode_step: logits requested but the model has no LM head");
   const int nsplit = attn_num_splits(m->max_seq, B, dm.Hk);
   Bufs bf;
-  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
+  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, st, bf));
   const size_t hbytes = (size_t)B * dm.D * 2;
   const bool want_logits = logits != nullptr;
   // a stream being captured by the caller records the eager launches
@@ -785,8 +819,8 @@ int decode_loop(r4q_ctx* ctx, const r4q_model* m, const void* hidden_in, int64_t
   R4Q_TRY(check_positions(m, start_pos, num_tokens));
   const int nsplit = attn_num_splits(m->max_seq, B, dm.Hk);
   Bufs bf;
-  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, bf));
   hipStream_t st = as_stream(stream);
+  R4Q_TRY(reserve(ctx, m, dm, B, nsplit, st, bf));
   int64_t* toks = static_cast<int64_t*>(tokens_out);
   void* sws = nullptr;
   if (scfg.temperature > 0.f) R4Q_TRY(sample_reserve(ctx, B, st, &sws));
@@ -844,8 +878,8 @@ extern "C" int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* 
   R4Q_TRY(check_positions(m, pos, 1));
   const int nsplit = attn_num_splits(m->max_seq, 1, dm.Hk);
   Bufs bf;
-  R4Q_TRY(reserve(ctx, m, dm, 1, nsplit, bf));
   hipStream_t st = as_stream(stream);
+  R4Q_TRY(reserve(ctx, m, dm, 1, nsplit, st, bf));
   R4Q_HIP_TRY(hipMemcpyAsync(bf.h, hidden_in, (size_t)dm.D * 2, hipMemcpyDeviceToDevice, st));
   std::vector<hipEvent_t> ev;
   std::vector<int> cat;

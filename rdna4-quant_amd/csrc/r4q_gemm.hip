@@ -1043,18 +1043,50 @@ struct SkLoop {
   }
 };
 
+// Balanced SiLU tail (SILU, tail.part != NULL): units 0 .. umain-1 (whole
+// rounds of 256) run one workgroup each over all of K; each of the other
+// units is cut along K into S pieces of kps steps (workgroups umain + u' S +
+// s), which leave fp32 partials and count in on the unit's counter; the last
+// piece to arrive sums the S partials in piece order and finishes the unit.
+// Without it the units past the last whole round (544 = 2 x 256 + 32 at I =
+// 17408) ran as a third workgroup on 32 CUs, which then finished a whole
+// unit after the rest.
+struct SkTail {
+  float* part = nullptr;  // [tail units][S][8 rows][64 tile rows] fp32
+  int* cnt = nullptr;     // [tail units] arrivals, zero before and after a launch
+  int umain = 0, S = 1, kps = 0;
+};
+
+// Device-coherent 32-bit load and store (agent scope: past the caches of the
+// other XCDs), for partials that workgroups hand to each other in a launch.
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int WBITS, int MR, bool SILU>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint32_t* __restrict__ SZ,
                                                           uint16_t* __restrict__ Y,
                                                           float* __restrict__ part, int M, int N,
-                                                          int K, int ntiles, int kps, int silu_I) {
+                                                          int K, int ntiles, int kps, int silu_I,
+                                                          SkTail tail) {
   static_assert(!SILU || MR == 8, "the SiLU epilogue maps 8 rows x 32 elements to 256 threads");
   using R = SkRing<WBITS, MR>;
   __shared__ __align__(16) uint8_t ring[kSkStages * R::kStage];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
+  int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
+  // SiLU tail piece: unit tile, piece sp of tail.S (workgroup-uniform)
+  const bool piece = SILU && tail.part && (int)blockIdx.x >= tail.umain;
+  if (piece) {
+    const int j = (int)blockIdx.x - tail.umain;
+    tile = tail.umain + j / tail.S;
+    sp = j % tail.S;
+    kps = tail.kps;
+  }
   const int n0 = SILU ? 32 * tile : tile * kSkTile;
   const int n1 = SILU ? silu_I + 32 * tile : n0 + 32;
   const int kt = K / R::kKS;
@@ -1088,13 +1120,47 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 #pragma clang fp contract(off)  // g / (1 + e^-g) * u in separately rounded steps
     __syncthreads();  // every wave is done with the ring, which now holds
     float* us = reinterpret_cast<float*>(ring);  // us[m][tile row], 8 x 64
-    if (g < 2) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) us[(4 * g + r) * 64 + 16 * wave + col] = h2f(f2h(acc[r]));
-    }
-    __syncthreads();
     const int m = threadIdx.x >> 5, i = threadIdx.x & 31;
-    const float gv = us[m * 64 + i], uv = us[m * 64 + 32 + i];
+    float gv, uv;
+    if (piece) {
+      // partials out as device-coherent stores, which every wave waits for
+      // before thread 0 counts the piece in; the last of the unit's S pieces
+      // resets the counter for the next launch and sums the partials
+      const int tu = tile - tail.umain;
+      float* tp = tail.part + ((int64_t)tu * tail.S + sp) * 512;
+      if (g < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st_agent(tp + (4 * g + r) * 64 + 16 * wave + col, acc[r]);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      int* last = reinterpret_cast<int*>(us + 512);
+      if (threadIdx.x == 0) {
+        int* c = tail.cnt + tu;
+        const int prev = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last = prev == tail.S - 1;
+        if (prev == tail.S - 1) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (*last == 0) return;
+      // the split reduce's arithmetic: fp32 sums in piece order, one fp16 rounding
+      const float* tb = tail.part + (int64_t)tu * tail.S * 512 + m * 64 + i;
+      float ga = ld_agent(tb), ua = ld_agent(tb + 32);
+      for (int z = 1; z < tail.S; ++z) {
+        ga += ld_agent(tb + z * 512);
+        ua += ld_agent(tb + z * 512 + 32);
+      }
+      gv = h2f(f2h(ga));
+      uv = h2f(f2h(ua));
+    } else {
+      if (g < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) us[(4 * g + r) * 64 + 16 * wave + col] = h2f(f2h(acc[r]));
+      }
+      __syncthreads();
+      gv = us[m * 64 + i];
+      uv = us[m * 64 + 32 + i];
+    }
     float v = gv / (1.0f + expf(-gv)) * uv;
 #pragma unroll
     for (int bit = 1; bit <= 16; bit <<= 1) {
@@ -1250,6 +1316,34 @@ size_t skinny_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
 }
 
 namespace {
+size_t skinny_tail_part_bytes(int64_t T, int64_t S) {
+  return ((size_t)T * S * 512 * 4 + 255) & ~(size_t)255;
+}
+size_t skinny_tail_cnt_bytes(int64_t T) { return ((size_t)T * 4 + 255) & ~(size_t)255; }
+
+// Tail plan of the unsplit SiLU GEMM (see SkTail) for I / 32 units over 256
+// CUs: the units past the last whole round of 256, each cut into S pieces
+// of kps K steps with S about 128 / tail units (measured at 32 tail units:
+// 4 pieces each 3.845 ms per batch-8 step, 2 / 3 / 8 / 16 pieces 3.935 /
+// 3.877 / 3.852 / 3.892 ms).  No tail
+// (part == NULL) without a workspace, below one round, on whole rounds, or
+// when a unit would not be cut.  Workspace: the counters, then the partials.
+SkTail skinny_tail_plan(int64_t I, int64_t K, int wbits, void* ws) {
+  SkTail t;
+  const int64_t units = I / 32, kt = K / (1024 / wbits);
+  const int64_t T = units % 256;
+  if (!ws || units <= 256 || T == 0) return t;
+  const int64_t S0 = std::min<int64_t>(kt, std::max<int64_t>(1, 128 / T));
+  const int64_t kps = (kt + S0 - 1) / S0, S = (kt + kps - 1) / kps;  // every piece non-empty
+  if (S < 2) return t;
+  t.umain = (int)(units - T);
+  t.S = (int)S;
+  t.kps = (int)kps;
+  t.cnt = static_cast<int*>(ws);  // counters first: the same place for every width
+  t.part = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + skinny_tail_cnt_bytes(T));
+  return t;
+}
+
 // silu_I > 0: N = 2 silu_I gate/up columns into y (M x silu_I) gated by
 // SiLU + FWHT-32: split (S > 1) and reduced by
 // gemm_skinny_reduce_silu_kernel, or unsplit (S == 1, M <= 8: checked by the
@@ -1257,7 +1351,7 @@ namespace {
 // S fp32 partial planes stay in ws (S > 1) for the consumer to sum.
 int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
                int64_t K, int wbits, hipStream_t st, void* ws, size_t ws_bytes, int64_t silu_I,
-               bool keep_part = false) {
+               bool keep_part = false, void* tail_ws = nullptr) {
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
@@ -1272,10 +1366,13 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   if (silu_I > 0 && S == 1) {  // unsplit: the SiLU gate in the epilogue
     R4Q_REQUIRE(M <= 8 && silu_I % 32 == 0 && N == 2 * silu_I,
                 "gate_up_silu: the unsplit epilogue takes at most 8 rows (M=%lld)", (long long)M);
+    const SkTail tl = skinny_tail_plan(silu_I, K, wbits, tail_ws);
+    const int64_t units = silu_I / 32;
+    const int64_t wgs = tl.part ? tl.umain + (units - tl.umain) * tl.S : units;
 #define R4Q_SKINNY_SILU(WB)                                                                      \
-  hipLaunchKernelGGL((gemm_skinny_kernel<WB, 8, true>), dim3((unsigned)(silu_I / 32)), dim3(256), \
-                     0, st, xp, wp, sp, yp, nullptr, (int)M, (int)N, (int)K,                     \
-                     (int)(silu_I / 32), kps, (int)silu_I)
+  hipLaunchKernelGGL((gemm_skinny_kernel<WB, 8, true>), dim3((unsigned)wgs), dim3(256), 0, st,   \
+                     xp, wp, sp, yp, nullptr, (int)M, (int)N, (int)K, (int)units, kps,           \
+                     (int)silu_I, tl)
     if (wbits == 4) R4Q_SKINNY_SILU(4);
     else if (wbits == 8) R4Q_SKINNY_SILU(8);
     else R4Q_SKINNY_SILU(16);
@@ -1284,7 +1381,7 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
   }
 #define R4Q_SKINNY(WB, MRR)                                                                    \
   hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR, false>), grid, dim3(256), 0, st, xp, wp, sp, \
-                     yp, part, (int)M, (int)N, (int)K, (int)ntiles, kps, 0)
+                     yp, part, (int)M, (int)N, (int)K, (int)ntiles, kps, 0, SkTail{})
   switch (wbits) {
     case 4:
       if (m8) R4Q_SKINNY(4, 8);
@@ -1341,6 +1438,26 @@ int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* 
   R4Q_REQUIRE(gemm_skinny_silu_ok(M, I, K, wbits, ws ? ws_bytes : 0),
               "gate_up_silu: needs I %% 32 == 0, and above 8 rows a workspace that splits K");
   return skinny_run(x, w, sz, y, M, 2 * I, K, wbits, st, ws, ws_bytes, I);
+}
+
+size_t skinny_silu_tail_bytes(int64_t I, int64_t K, int wbits) {
+  int dummy = 0;
+  const SkTail t = skinny_tail_plan(I, K, wbits, &dummy);
+  if (!t.part) return 0;
+  const int64_t T = I / 32 - t.umain;
+  return skinny_tail_cnt_bytes(T) + skinny_tail_part_bytes(T, t.S);
+}
+
+size_t skinny_silu_tail_cnt_bytes(int64_t I) {
+  const int64_t units = I / 32;
+  return units > 256 && units % 256 ? skinny_tail_cnt_bytes(units % 256) : 0;
+}
+
+int gemm_skinny_silu_tail_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                                 int64_t I, int64_t K, int wbits, hipStream_t st, void* tail_ws) {
+  R4Q_REQUIRE(M <= 8 && gemm_skinny_silu_ok(M, I, K, wbits, 0),
+              "gate_up_silu: the unsplit epilogue takes at most 8 rows and I %% 32 == 0");
+  return skinny_run(x, w, sz, y, M, 2 * I, K, wbits, st, nullptr, 0, I, false, tail_ws);
 }
 
 // The ring kernel addresses X, W and the scale words with 32-bit byte offsets.

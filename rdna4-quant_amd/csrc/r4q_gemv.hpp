@@ -79,6 +79,16 @@ bool gemm_skinny_silu_ok(int64_t M, int64_t I, int64_t K, int wbits, size_t ws_b
 int gemm_skinny_silu_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
                             int64_t I, int64_t K, int wbits, hipStream_t st, void* ws,
                             size_t ws_bytes);
+// The same unsplit SiLU GEMM (M <= 8) with the units past the last whole
+// round of 256 cut along K into pieces spread over the CUs; tail_ws holds
+// skinny_silu_tail_bytes(I, K, wbits) bytes, of which the first
+// skinny_silu_tail_cnt_bytes(I) (arrival counters, the same for every
+// width) are zero before the call and after it.  tail_ws == NULL: the
+// plain unsplit launch.
+size_t skinny_silu_tail_bytes(int64_t I, int64_t K, int wbits);
+size_t skinny_silu_tail_cnt_bytes(int64_t I);
+int gemm_skinny_silu_tail_launch(const void* x, const void* w, const void* sz, void* y, int64_t M,
+                                 int64_t I, int64_t K, int wbits, hipStream_t st, void* tail_ws);
 
 // Workspace bytes gemm_launch can use for a shape (0: none), over both the
 // skinny (M <= 16) and the tiled paths.

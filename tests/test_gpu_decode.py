@@ -60,9 +60,10 @@ def test_qwen3_width_two_layers_vs_oracle(dev):
 
 def test_qwen3_width_batch8_step_vs_oracle(dev):
     """Batch 8 at full Qwen3-14B width: skinny MFMA GEMMs with the step's own
-    split-K workspace, the gate/up split reduce applying SiLU + FWHT-32 (both
-    layers, INT4 and INT8), batched row norms; every row against the oracle
-    under KV teacher forcing."""
+    split-K workspace, the gate/up GEMM applying SiLU + FWHT-32 in its
+    epilogue, its 32 units past two whole rounds of 256 cut along K into
+    pieces whose last arrival sums them (both layers, INT8 and INT4), batched
+    row norms; every row against the oracle under KV teacher forcing."""
     bits = {(0, "gu"): 8, (1, "down"): 8, (1, "qkv"): 8}
     m = build(dev, D=5120, I=17408, H=40, Hk=8, L=2, vocab=4096, max_seq=96, seed=13, bits=bits,
               batch=8, fill=60, kv_scale=True)
