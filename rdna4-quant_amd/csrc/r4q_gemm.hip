@@ -875,7 +875,9 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const uint16_t*
 // the weights at ~5.6-6 TB/s where 16 rows x 64 B per instruction -- the
 // MFMA B-fragment layout loaded straight into registers -- measured
 // 4.4-4.9 TB/s), the rows' (scale, zero) words and the matching slice of the
-// MR activation rows.  kSkStages steps are in flight; one barrier per step
+// MR activation rows.  kSkStages ring stages, stages - 1 steps in flight
+// (kSkDeepStages stages when the grid has at most one workgroup per CU, whose
+// LDS then allows it); one barrier per step
 // (the ring of gemm_ring_kernel).  Per step each wave runs KS/32 MFMA
 // 16x16x32 tiles: B = its 16 weight rows dequantised from LDS (skinny_b),
 // A = the activation rows (skinny_a's element order), C = 16 activation
@@ -894,7 +896,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const uint16_t*
 // does not depend on the tile it sits in, so the result equals the unsplit
 // GEMM followed by that kernel bit for bit.
 constexpr int kSkTile = 64;   // weight rows per workgroup
-constexpr int kSkStages = 3;  // steps in flight
+constexpr int kSkStages = 3;      // ring stages (stages - 1 steps in flight)
+// at most one workgroup per CU; against 3 stages the batch-8 step measured
+// -19 us with 4, +44 us with 5 and +100 us with 6
+constexpr int kSkDeepStages = 4;
 constexpr int kSkMaxSplits = 8;
 
 template <int WBITS, int MR>
@@ -985,10 +990,10 @@ struct SkCopy {
 // argument (the loop is unrolled by the ring depth), so that the LDS reads
 // address each stage through their immediate offset from per-lane offsets
 // computed once.
-template <int WBITS, int MR>
+template <int WBITS, int MR, int D>
 struct SkLoop {
   using R = SkRing<WBITS, MR>;
-  static constexpr int D = kSkStages;
+  static_assert(D >= 3 && (D - 2) * R::kPer <= 63, "ring depth: copy waits fit vmcnt");
   lds8* ring;
   const uint16_t* X;
   const uint8_t* W;
@@ -1027,19 +1032,28 @@ struct SkLoop {
     }
   }
 
+  // steps i, i+1, ... from ring stage ST to D-1 (one round of the ring)
+  template <int ST>
+  __device__ __forceinline__ void round_from(int i) {
+    step<ST>(i);
+    if constexpr (ST + 1 < D) round_from<ST + 1>(i + 1);
+  }
+  // the last nk - i < D steps, from stage 0
+  template <int ST>
+  __device__ __forceinline__ void tail_from(int i) {
+    if (i < nk) {
+      step<ST>(i);
+      if constexpr (ST + 2 < D) tail_from<ST + 1>(i + 1);
+    }
+  }
+
   __device__ __forceinline__ void run() {
 #pragma unroll
     for (int s = 0; s < D - 1; ++s)
       cp.issue(ring + s * R::kStage, X, W, SZ, kb0 + min(s, nk - 1), wave);
-    static_assert(D == 3, "the loop below is unrolled by the ring depth");
     int i = 0;
-    for (; i + 3 <= nk; i += 3) {
-      step<0>(i);
-      step<1>(i + 1);
-      step<2>(i + 2);
-    }
-    if (i < nk) step<0>(i);
-    if (i + 1 < nk) step<1>(i + 1);
+    for (; i + D <= nk; i += D) round_from<0>(i);
+    tail_from<0>(i);
   }
 };
 
@@ -1066,7 +1080,7 @@ __device__ __forceinline__ void st_agent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int WBITS, int MR, bool SILU>
+template <int WBITS, int MR, bool SILU, int D = kSkStages>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ X,
                                                           const uint8_t* __restrict__ W,
                                                           const uint32_t* __restrict__ SZ,
@@ -1076,7 +1090,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
                                                           SkTail tail) {
   static_assert(!SILU || MR == 8, "the SiLU epilogue maps 8 rows x 32 elements to 256 threads");
   using R = SkRing<WBITS, MR>;
-  __shared__ __align__(16) uint8_t ring[kSkStages * R::kStage];
+  __shared__ __align__(16) uint8_t ring[D * R::kStage];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int tile = blockIdx.x % ntiles, sp = blockIdx.x / ntiles;
   // SiLU tail piece: unit tile, piece sp of tail.S (workgroup-uniform)
@@ -1094,7 +1108,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   const int wrow = 16 * wave + col;                   // this lane's weight row in the tile
   const int xr = col % MR;                            // activation row (rows >= MR: duplicates)
 
-  SkLoop<WBITS, MR> lp;
+  SkLoop<WBITS, MR, D> lp;
   lp.ring = (lds8*)ring;
   lp.X = X;
   lp.W = W;
@@ -1379,9 +1393,13 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
 #undef R4Q_SKINNY_SILU
     return launch_status("gemm_skinny_silu");
   }
+  const bool deep = ntiles * S <= 256;  // one workgroup per CU: LDS for a deeper ring
+#define R4Q_SKINNY_D(WB, MRR, DD)                                                              \
+  hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR, false, DD>), grid, dim3(256), 0, st, xp, wp, \
+                     sp, yp, part, (int)M, (int)N, (int)K, (int)ntiles, kps, 0, SkTail{})
 #define R4Q_SKINNY(WB, MRR)                                                                    \
-  hipLaunchKernelGGL((gemm_skinny_kernel<WB, MRR, false>), grid, dim3(256), 0, st, xp, wp, sp, \
-                     yp, part, (int)M, (int)N, (int)K, (int)ntiles, kps, 0, SkTail{})
+  if (deep) R4Q_SKINNY_D(WB, MRR, kSkDeepStages);                                            \
+  else R4Q_SKINNY_D(WB, MRR, kSkStages)
   switch (wbits) {
     case 4:
       if (m8) R4Q_SKINNY(4, 8);
@@ -1396,6 +1414,7 @@ int skinny_run(const void* x, const void* w, const void* sz, void* y, int64_t M,
       else R4Q_SKINNY(16, 16);
   }
 #undef R4Q_SKINNY
+#undef R4Q_SKINNY_D
   R4Q_TRY(launch_status("gemm_skinny"));
   if (keep_part) return R4Q_OK;
   if (silu_I > 0) {
