@@ -79,6 +79,30 @@ def test_qwen3_width_batch8_step_vs_oracle(dev):
         assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
 
 
+def test_batch8_gate_up_tail_pieces_vs_oracle(dev):
+    """I = 9600: 300 SiLU units, one whole round of 256 and 44 tail units
+    that the batched gate/up GEMM cuts along K into two pieces each (INT8
+    layer 0, INT4 layer 1); every row against the oracle, and a second step
+    on the same inputs bit-identical to the first (each launch leaves the
+    tail's arrival counters at zero for the next)."""
+    bits = {(0, "gu"): 8}
+    m = build(dev, D=1024, I=9600, H=16, Hk=8, L=2, vocab=512, max_seq=48, seed=31, bits=bits,
+              batch=8, fill=20)
+    nsplit, fused = plan(m, 8)
+    assert fused == 2, fused
+    h = _hidden(m, 32, rows=8)
+    pos = 20
+    first = step_logits(m, h.to(dev), pos).cpu()
+    second = step_logits(m, h.to(dev), pos).cpu()
+    assert torch.equal(first.view(torch.int16), second.view(torch.int16))
+    logits = first.float().numpy().reshape(8, -1)
+    assert np.all(np.isfinite(logits))
+    _, want, n, total = oracle_batch_forced(m, h.numpy().reshape(8, -1), pos)
+    assert n <= 0.05 * total, f"{n} of {total} KV codes differ"
+    for b in range(8):
+        assert rel_l2(logits[b], want[b]) <= TOL, (b, rel_l2(logits[b], want[b]))
+
+
 def test_qwen3_width_batch8_ctx2048_step_vs_oracle(dev):
     """Batch 8 at ctx 2048 (position 2048, cache capacity 2088): 8 attention
     splits per (sequence, KV head) whose prologue sums the qkv split partials,
