@@ -509,8 +509,8 @@ __global__ __launch_bounds__(256) void attn_mfma_kernel(
 //   m* = max_s m_s,  out = sum_s e^(m_s-m*) o_s / sum_s e^(m_s-m*) l_s.
 // The two half-waves take the even and the odd splits, lane j of a half
 // owning dims 4j .. 4j+3 (16-byte loads: one instruction reads two splits'
-// o), and add their sums at the end.  CH splits per round (16, 18, 24, 32
-// or 64: the smallest covering the split count) with a running maximum;
+// o), and add their sums at the end.  CH splits per round (8, 16, 18, 24,
+// 32 or 64: the smallest covering the split count) with a running maximum;
 // every load of a round is issued before any arithmetic; slots past the
 // last split re-read it and get weight 0, so CH does not change the result.
 template <int CH>
@@ -642,7 +642,10 @@ int launch_flash_decode(const void* q, int64_t q_stride, const void* k_cache, co
     const dim3 mg(grouped ? (unsigned)(kXcds * G) : (unsigned)G,
                   grouped ? (unsigned)(npair / kXcds) : (unsigned)npair);
     auto* o16 = static_cast<uint16_t*>(out);
-    if (nsplit <= 16)
+    if (nsplit <= 8)
+      hipLaunchKernelGGL(attn_merge_kernel<8>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
+                         G, nsplit);
+    else if (nsplit <= 16)
       hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, part, o16, out_stride, (int)H,
                          G, nsplit);
     else if (nsplit <= 18)
