@@ -868,6 +868,441 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const uint16_t*
 }
 
 // ---------------------------------------------------------------------
+// Prefill GEMM with specialised waves (INT4, M >= 256, N % 128 == 0,
+// K % 256 == 0; selected by the gemm_kernel knob, see use_spec for how it
+// measures against the ring kernel).  A workgroup of 8 waves owns a 256 x
+// 128 output tile:
+//  * waves 0-3 ("MFMA waves") copy X of every K step global -> LDS
+//    (global_load_lds, 64 rows each) and otherwise only read fragments from
+//    LDS and issue MFMAs: wave c computes rows 128 (c >> 1) .. +127 x
+//    columns 64 (c & 1) .. +63 (8 x 4 v_mfma_f32_16x16x32_f16 tiles, 128
+//    fp32 accumulators per lane);
+//  * waves 4-7 ("dequantisation waves") copy the raw weights and (scale,
+//    zero) words of every super-step of 8 K steps (128 bytes of each weight
+//    row: whole cache lines) global -> LDS, and dequantise: each lane turns
+//    half a row's 32-element block of K step g + 3 into fp16 in a ring of B
+//    stages, from raw bytes it read from LDS in the step before (its own
+//    wave's copies: rows 32 p .. 32 p + 31 of wave p).
+// Waves c and c + 4 share a SIMD, so the dequantisation of one runs while
+// the other's MFMAs execute instead of serialising with them in one wave.
+// One barrier per K step for all 8 waves; the ring stages are indexed by
+// the workgroup's running K step, so the pipeline runs on across the tiles
+// of a stream-K range.  Invariants (barrier B_g opens step g):
+//  * X and B of step g + 1 are complete at B_g (the MFMA waves read them
+//    during step g); X copies of step g + 4 go out in step g into the stage
+//    step g used; B of step g + 3 is written in step g into the stage of
+//    step g - 1 and waited for one step later (its consumers read it after
+//    B_g+2);
+//  * the raw weights of super-step s + 1 go out in step 8 s - 4, after the
+//    last raw read of the buffer they replace (super-step s - 1), and are
+//    waited for in step 8 s + 4, before the first read of their own.
+// The dequantised values equal r4q_dequant_int4 bit for bit and every
+// output element sees the same MFMA sequence as in gemm_ring_kernel, so
+// whole tiles are bit-identical to it.  Shared tiles leave fp16 partials in
+// the accumulator layout, summed by gemm_spec_reduce_kernel in segment
+// order.
+constexpr int SBM = 256, SBN = 128;
+constexpr int kSpecWaves = 8;  // 4 MFMA waves, then 4 dequantisation waves
+constexpr int kSpecThreads = 64 * kSpecWaves;
+constexpr int kSpecKS = 8;     // K steps per weight super-step (INT4: 128 bytes of a row)
+constexpr int kSpecXSt = 4;    // X stages: copies of step g + 4 issued in step g
+constexpr int kSpecBSt = 4;    // dequantised B stages: step g + 3 written in step g
+struct SpecRing {
+  static constexpr int kX = SBM * RBK * 2;             // 16 KB
+  static constexpr int kB = SBN * RBK * 2;             // 8 KB
+  static constexpr int kW = SBN * 128;                 // 16 KB of raw INT4 per super-step
+  static constexpr int kS = SBN * kSpecKS * 4;         // 4 KB of (scale, zero) words
+  static constexpr int kBOff = kSpecXSt * kX;
+  static constexpr int kWOff = kBOff + kSpecBSt * kB;
+  static constexpr int kSOff = kWOff + 2 * kW;
+  static constexpr int kBytes = kSOff + 2 * kS;        // 136 KB
+  static constexpr int kXc = SBM / 4 / 16;             // X copies per MFMA wave per step: 4
+  static constexpr int kWc = SBN / 4 / 8 + SBN / 4 * kSpecKS * 4 / 256;  // per super-step: 4 + 4
+};
+
+// Raw weights and (scale, zero) words of the super-step starting at K step
+// kb for tile rows 32 p .. 32 p + 31 (dequantisation wave p): 8 rows x 128
+// bytes per copy, chunk q of row r at slot q ^ wswz(r); the words of a row
+// in natural order (32 bytes per row).
+__device__ __forceinline__ void spec_w_issue(lds8* wb, lds8* sb, const uint8_t* __restrict__ W,
+                                             const uint32_t* __restrict__ SZ, int N, int K,
+                                             int n0, int kb, int p, int lane) {
+  const uint32_t ksz = K / 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r0 = 32 * p + 8 * q;
+    const int r = r0 + (lane >> 3);
+    const int qg = (lane & 7) ^ wswz(r);
+    const uint32_t n = min(n0 + r, N - 1);
+    copy16s(W, n * (uint32_t)(K / 2) + (uint32_t)(kb + qg) * 16u, wb + r0 * 128);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r0 = 32 * p + 8 * q;
+    const uint32_t n = min(n0 + r0 + (lane >> 3), N - 1);
+    copy4s(SZ, 4u * (n * ksz + (uint32_t)(kb + (lane & 7))), sb + r0 * 32);
+  }
+}
+
+// Raw input of one lane's dequantisation: 16 nibbles and the block's
+// (scale, zero) word.
+struct SpecRaw {
+  u2_t w;
+  uint32_t s2;
+};
+
+// Position pos of a super-step (one K step) for tile row r = 32 p + lane /
+// 2, elements 16 h .. 16 h + 15 of its block (h = lane & 1).
+__device__ __forceinline__ SpecRaw spec_raw(const lds8* wb, const lds8* sb, int pos, int p,
+                                            int lane) {
+  const int r = 32 * p + (lane >> 1), h = lane & 1;
+  return SpecRaw{lds_ld<u2_t>(wb + r * 128 + ((pos ^ wswz(r)) << 4) + 8 * h),
+                 lds_ld<uint32_t>(sb + r * 32 + 4 * pos)};
+}
+
+// fp16 weights of a lane's raw input as pieces 2 h and 2 h + 1 of row r in
+// a B stage (64 bytes per row, piece P at slot P ^ ((r >> 1) & 3): the X
+// layout, so that the MFMA waves read B fragments like X fragments).
+__device__ __forceinline__ void spec_dequant(lds8* bs, const SpecRaw& in, int p, int lane) {
+  const int r = 32 * p + (lane >> 1), h = lane & 1;
+  const uint32_t sbits = in.s2 & 0xFFFFu, zb = in.s2 >> 16;
+  const h2_t sc = as_h2(sbits | (sbits << 16));
+  const h2_t nz = -(as_h2(0x64006400u) + as_h2(zb | (zb << 16)));  // -(1024 + zp), exact
+  u4_t o[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const uint32_t w = in.w[d], w4 = w >> 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[d][k] = as_u32((as_h2(nib_pair(w, w4, k)) + nz) * sc);
+  }
+  const int sw = (r >> 1) & 3;
+  lds8* row = bs + r * 64;
+  *(__attribute__((address_space(3))) u4_t*)(row + 16 * ((2 * h) ^ sw)) = o[0];
+  *(__attribute__((address_space(3))) u4_t*)(row + 16 * ((2 * h + 1) ^ sw)) = o[1];
+}
+
+// Unit range of a ring / specialised workgroup: blocks [0, dp) take tile b
+// whole, the sk stream-K workgroups share the units of the other tiles
+// (consecutive ones on one XCD); w = the stream-K index.
+__device__ __forceinline__ void sk_range(int b, int dp, int sk, int U, int tiles, int64_t& lo,
+                                         int64_t& hi, int64_t& TU, int& w) {
+  TU = 0;
+  w = 0;
+  if (b < dp) {
+    lo = (int64_t)b * U;
+    hi = lo + U;
+  } else {
+    const int bb = b - dp;
+    w = (sk % 8 == 0) ? (b % 8) * (sk / 8) + bb / 8 : bb;
+    TU = (int64_t)(tiles - dp) * U;
+    lo = (int64_t)dp * U + sk_lo(w, TU, sk);
+    hi = (int64_t)dp * U + sk_lo(w + 1, TU, sk);
+  }
+}
+
+// Position in a workgroup's K steps as (tile, unit of the tile, step of the
+// unit), advanced one step at a time without divisions.
+struct SpecCursor {
+  int tile, unit, pos;
+  __device__ __forceinline__ void init(int u, int U) {
+    tile = u / U;
+    unit = u - tile * U;
+    pos = 0;
+  }
+  __device__ __forceinline__ void next(int U) {
+    if (++pos == kSpecKS) {
+      pos = 0;
+      if (++unit == U) {
+        unit = 0;
+        ++tile;
+      }
+    }
+  }
+  __device__ __forceinline__ int kb() const { return unit * kSpecKS + pos; }
+};
+
+// Barrier that waits only for this wave's LDS accesses older than its last N.
+template <int N>
+__device__ __forceinline__ void ring_barrier_lgkm() {
+  asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__global__ __launch_bounds__(kSpecThreads, 1) void gemm_spec_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+    const uint32_t* __restrict__ SZ, uint16_t* __restrict__ Y, uint16_t* __restrict__ part, int M,
+    int N, int K, int dp, int sk, int U, int maxseg) {
+  using R = SpecRing;
+  __shared__ __align__(16) uint8_t ring[R::kBytes];
+  lds8* rb = (lds8*)ring;
+  asm volatile("" : "+s"(rb));  // a value the compiler cannot see (see gemm_ring_kernel)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int ntn = N / SBN;
+  const int tiles = ntn * ((M + SBM - 1) / SBM);
+  int64_t lo, hi, TU;
+  int w;
+  sk_range(blockIdx.x, dp, sk, U, tiles, lo, hi, TU, w);
+  // K steps of this workgroup: whole units of kSpecKS steps (K % 256 == 0)
+  const int G = (int)(hi - lo) * kSpecKS;
+  if (G <= 0) return;  // workgroup-uniform: no wave reaches a barrier
+  const int ulo = (int)lo;
+  if (wave >= 4) {
+    // ----------------------------------------------- dequantisation waves
+    const int p = wave - 4;
+    const int S = G / kSpecKS;  // super-steps
+    auto wcopy = [&](int s) {   // raw weights of super-step s (clamped) into buffer s & 1
+      const int u = ulo + min(s, S - 1), tile = u / U;
+      spec_w_issue(rb + R::kWOff + (s & 1) * R::kW, rb + R::kSOff + (s & 1) * R::kS, W, SZ, N, K,
+                   (tile % ntn) * SBN, (u - tile * U) * kSpecKS, p, lane);
+    };
+    auto raw = [&](int g) {  // this lane's raw input of step g
+      const int s = g / kSpecKS;
+      return spec_raw(rb + R::kWOff + (s & 1) * R::kW, rb + R::kSOff + (s & 1) * R::kS,
+                      g % kSpecKS, p, lane);
+    };
+    auto bstage = [&](int g) { return rb + R::kBOff + (g % kSpecBSt) * R::kB; };
+    wcopy(0);
+    wcopy(1);
+    wait_copies<R::kWc>();  // super-step 0 (this wave's rows)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < G) spec_dequant(bstage(j), raw(j), p, lane);
+    SpecRaw nx = raw(min(3, G - 1));  // step 3 is in super-step 0
+    ring_barrier();                    // B_-1: B of steps 0-2 complete
+    // Every step issues the same 4 LDS accesses (2 writes, 2 reads; past
+    // the last step they repeat step G - 1 into stages nobody reads again),
+    // so that the barrier's count below is exact.
+    for (int g = 0; g < G; ++g) {
+      // B of step g + 1 (written in step g - 2) complete; the 4 accesses of
+      // step g - 1 may still be in flight
+      ring_barrier_lgkm<4>();  // B_g
+      // keeps the dequantisation below the barrier: hoisted above it, its
+      // wait for the raw reads would also wait for the previous step's writes
+      __builtin_amdgcn_sched_barrier(0);
+      spec_dequant(bstage(g + 3), nx, p, lane);
+      // the raw buffer of super-step (g + 4) / 8 - 1 was last read in step
+      // g - 1 (its registers were consumed just above); past the last
+      // super-step the copies repeat it (the same bytes)
+      if (g >= 4 && (g + 4) % kSpecKS == 0) wcopy((g + 4) / kSpecKS + 1);
+      // the first raw read of a super-step: its copies (issued 8 steps
+      // ago) landed; only the next super-step's may be in flight
+      if (g + 4 < G && (g + 4) % kSpecKS == 0) wait_copies<R::kWc>();
+      nx = raw(min(g + 4, G - 1));
+    }
+    wait_copies<0>();  // no copy may land after the workgroup ends
+    return;
+  }
+  // -------------------------------------------------------------- MFMA waves
+  const int c = lane & 15, gq = lane >> 4;
+  const int sw = 16 * (gq ^ ((c >> 1) & 3));
+  const int cm = 128 * (wave >> 1), cn = 64 * (wave & 1);
+  const int xoff = (cm + c) * 64 + sw;  // A fragment i8 at + 1024 i8
+  const int boff = (cn + c) * 64 + sw;  // B fragment j at + 1024 j
+  // X copies: rows 64 wave + 16 q + lane / 4, the 16-byte piece held by LDS
+  // slot lane & 3 (X layout); per-lane byte offsets for the current M tile
+  // (rows clamped into the matrix), the K step on the scalar base
+  uint32_t xo[R::kXc];
+  int xm0 = -1;
+  auto xcopy = [&](const SpecCursor& cur, int g) {
+    const int m0 = (cur.tile / ntn) * SBM;
+    if (m0 != xm0) {
+      xm0 = m0;
+#pragma unroll
+      for (int q = 0; q < R::kXc; ++q) {
+        const int row = 64 * wave + 16 * q + (lane >> 2);
+        const int pc = (lane & 3) ^ ((row >> 1) & 3);
+        xo[q] = 2u * ((uint32_t)min(m0 + row, M - 1) * (uint32_t)K + 8u * pc);
+      }
+    }
+    const uint16_t* xb = X + (int64_t)__builtin_amdgcn_readfirstlane(cur.kb()) * RBK;
+    lds8* st = rb + (g % kSpecXSt) * R::kX + 64 * 64 * wave;
+#pragma unroll
+    for (int q = 0; q < R::kXc; ++q) copy16s(xb, xo[q], st + 1024 * q);
+  };
+  SpecCursor xc, cc;  // X copy step, compute step
+  xc.init(ulo, U);
+  cc.init(ulo, U);
+  int ng = 0;  // the step xc stands at (stops at G - 1)
+#pragma unroll
+  for (int s = 0; s < kSpecXSt; ++s) {
+    xcopy(xc, s);
+    if (ng < G - 1) {
+      xc.next(U);
+      ++ng;
+    }
+  }
+  f4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  // End of step g: the last step of a unit that closes the tile or the
+  // workgroup's range ends a segment, whose results go out (whole tile:
+  // fp16 outputs; shared tile: an fp16 partial) before the accumulators
+  // restart.
+  auto finish = [&](int g) {
+    const SpecCursor cur = cc;
+    cc.next(U);
+    if (cur.pos != kSpecKS - 1 || (cur.unit != U - 1 && g + 1 != G)) return;
+    const int tile = cur.tile;
+    const int64_t ua = max<int64_t>(lo, (int64_t)tile * U);
+    const int64_t ub = (int64_t)tile * U + cur.unit + 1;
+    const int m0 = (tile / ntn) * SBM, n0 = (tile % ntn) * SBN;
+    int tq = lane;
+    asm volatile("" : "+v"(tq));
+    if (ua == (int64_t)tile * U && ub == (int64_t)(tile + 1) * U) {
+      // C fragment: lane holds rows 4 g + r of an M-block, column c of an N-block
+      const int ec = tq & 15, eg = tq >> 4;
+#pragma unroll
+      for (int i8 = 0; i8 < 8; ++i8)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = n0 + cn + 16 * j + ec;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + cm + 16 * i8 + 4 * eg + r;
+            if (row < M) Y[(int64_t)row * N + col] = f2h(acc[i8][j][r]);
+          }
+        }
+    } else {
+      // fp16 partial in the accumulator layout: the 8 values of N-blocks 2 jp
+      // and 2 jp + 1 of (wave, i8, lane) as one 16-byte piece at
+      // ((wave * 8 + i8) * 2 + jp) * 64 + lane; gemm_spec_reduce_kernel reads it
+      const int tl = tile - dp;
+      const int j = w - sk_owner((int64_t)tl * U, TU, sk);
+      u4_t* pt = reinterpret_cast<u4_t*>(part + ((int64_t)tl * maxseg + j) * (SBM * SBN));
+      pt += wave * (8 * 2 * 64) + tq;
+#pragma unroll
+      for (int i8 = 0; i8 < 8; ++i8)
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          const f4_t a = acc[i8][2 * jp], d = acc[i8][2 * jp + 1];
+          pt[(i8 * 2 + jp) * 64] = u4_t{cvt_pk_h(a[0], a[1]), cvt_pk_h(a[2], a[3]),
+                                        cvt_pk_h(d[0], d[1]), cvt_pk_h(d[2], d[3])};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  // A step: the fragments of step g + 1 are requested first (into the other
+  // register set, so that nothing waits for them before the next barrier),
+  // then the 32 MFMAs of step g.
+  struct Frag {
+    h8_t a[8], b[4];
+  };
+  auto cstep = [&](int g, const Frag& cur, Frag& nxt) {
+    // X of step g + 1 landed (younger: the copies of steps g + 2 .. g + kSpecXSt - 1)
+    wait_copies<(kSpecXSt - 2) * R::kXc>();
+    ring_barrier();  // B_g: step g + 1's stages complete, this wave's reads of step g done
+    xcopy(xc, g + kSpecXSt);  // into the stage step g used (clamped to step G - 1)
+    if (ng < G - 1) {
+      xc.next(U);
+      ++ng;
+    }
+    // fragments of step g + 1 (after the last step: a stage nobody writes
+    // any more, read and never used)
+    const lds8* xs = rb + ((g + 1) % kSpecXSt) * R::kX + xoff;
+    const lds8* bs = rb + R::kBOff + ((g + 1) % kSpecBSt) * R::kB + boff;
+#pragma unroll
+    for (int i8 = 0; i8 < 8; ++i8) nxt.a[i8] = lds_ld<h8_t>(xs + 1024 * i8);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nxt.b[j] = lds_ld<h8_t>(bs + 1024 * j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i8 = 0; i8 < 8; ++i8)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i8][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.a[i8], cur.b[j], acc[i8][j], 0, 0, 0);
+    finish(g);
+  };
+  Frag f0, f1;
+  wait_copies<(kSpecXSt - 1) * R::kXc>();  // X of step 0
+  ring_barrier();                           // B_-1
+#pragma unroll
+  for (int i8 = 0; i8 < 8; ++i8) f0.a[i8] = lds_ld<h8_t>(rb + xoff + 1024 * i8);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f0.b[j] = lds_ld<h8_t>(rb + R::kBOff + boff + 1024 * j);
+  for (int g = 0; g < G; g += 2) {  // G is a multiple of kSpecKS
+    cstep(g, f0, f1);
+    cstep(g + 1, f1, f0);
+  }
+}
+
+// Y = fp16(sum over the segments of each shared 256 x 128 tile, in segment
+// order, in fp32) from the partials of gemm_spec_kernel: a thread takes
+// lanes 16 g + 4 q .. + 3 of one (wave, i8, jp) piece row -- rows 128 (wave
+// >> 1) + 16 i8 + 4 g .. + 3 x columns 64 (wave & 1) + 16 j + 4 q .. + 3 for
+// j = 2 jp, 2 jp + 1 -- and writes 4 x 8 outputs (the arithmetic of
+// gemm_splitk_reduce_kernel).
+constexpr int kSpecRedThreadsPerTile = SBM * SBN / 32;
+__global__ __launch_bounds__(256) void gemm_spec_reduce_kernel(const uint16_t* __restrict__ part,
+                                                               uint16_t* __restrict__ Y, int M,
+                                                               int N, int dp, int sk, int U,
+                                                               int maxseg) {
+  const int gt = blockIdx.x * 256 + threadIdx.x;
+  const int tl = gt / kSpecRedThreadsPerTile, x = gt % kSpecRedThreadsPerTile;
+  const int q = x & 3, g = (x >> 2) & 3, jp = (x >> 4) & 1, i8 = (x >> 5) & 7, wv = x >> 8;
+  const int ntn = N / SBN;
+  const int tiles = ntn * ((M + SBM - 1) / SBM);
+  const int64_t TU = (int64_t)(tiles - dp) * U;
+  const int w0 = sk_owner((int64_t)tl * U, TU, sk);
+  const int w1 = sk_owner((int64_t)tl * U + U - 1, TU, sk);
+  if (w1 == w0) return;  // written whole by one workgroup
+  const int tile = dp + tl;
+  const int row0 = (tile / ntn) * SBM + 128 * (wv >> 1) + 16 * i8 + 4 * g;
+  const int colb = (tile % ntn) * SBN + 64 * (wv & 1) + 32 * jp + 4 * q;  // N-block 2 jp
+  if (row0 >= M) return;
+  const int nseg = w1 - w0 + 1;
+  const u4_t* p = reinterpret_cast<const u4_t*>(part + (int64_t)tl * maxseg * (SBM * SBN)) +
+                  ((wv * 8 + i8) * 2 + jp) * 64 + 16 * g + 4 * q;
+  constexpr int64_t kSeg = SBM * SBN / 8;  // 16-byte pieces per segment
+  float v[2][4][4];  // v[b][l][r]: N-block 2 jp + b, column 4q + l, row 4g + r
+  auto add = [&](const u4_t (&t)[4], bool first) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t wd = t[l][2 * b + h];
+          const float lo = h2f((uint16_t)(wd & 0xFFFFu)), hi = h2f((uint16_t)(wd >> 16));
+          v[b][l][2 * h] = first ? lo : v[b][l][2 * h] + lo;
+          v[b][l][2 * h + 1] = first ? hi : v[b][l][2 * h + 1] + hi;
+        }
+  };
+  {
+    u4_t t[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) t[l] = p[l];
+    add(t, true);
+  }
+  for (int j0 = 1; j0 < nseg; j0 += 4) {
+    u4_t t[4][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int l = 0; l < 4; ++l) t[s][l] = p[(int64_t)min(j0 + s, nseg - 1) * kSeg + l];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      if (j0 + s < nseg) add(t[s], false);
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int col0 = colb + 16 * b;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (row0 + r >= M) break;
+      uint16_t* y = Y + (int64_t)(row0 + r) * N + col0;
+      const uint32_t lo = (uint32_t)f2h(v[b][0][r]) | ((uint32_t)f2h(v[b][1][r]) << 16);
+      const uint32_t hi = (uint32_t)f2h(v[b][2][r]) | ((uint32_t)f2h(v[b][3][r]) << 16);
+      *reinterpret_cast<u2_t*>(y) = u2_t{lo, hi};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------
 // Skinny GEMM for 2 <= M <= 16 rows (batched decode) through an LDS ring.
 // A workgroup (4 waves) owns 64 weight rows (16 per wave) and a range of K
 // steps; each step stages, by global->LDS copies, 128 bytes of every weight
@@ -1504,7 +1939,9 @@ static int64_t host_sk_owner(int64_t u, int64_t TU, int64_t sk) {
   return w;
 }
 
-RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+// dp / sk split of `tiles` tiles of U units each (see ring_plan), with fp16
+// partials of tile_elems elements per (shared tile, segment).
+static RingPlan split_plan(int64_t tiles, int U, int64_t tile_elems, size_t ws_bytes) {
   // Every CU gets the same number of K units: the tiles of the full rounds
   // of 256 workgroups are computed whole, the remaining tiles' units are
   // shared by 256 stream-K workgroups (each then writes at most two fp32
@@ -1513,10 +1950,8 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
   // at least 7/8 full: the partials and their reduce then cost what the idle
   // CUs would (the LM head of a 512-token prompt, 1188 tiles in 5 rounds:
   // 1109 us whole, 1116 us shared).
-  const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
-  const int KS = wbits == 4 ? Ring<4>::KS : wbits == 8 ? Ring<8>::KS : Ring<16>::KS;
   RingPlan pl;
-  pl.U = (int)((K / RBK + KS - 1) / KS);
+  pl.U = U;
   int64_t dp = tiles, sk = 0;
   const int v = tuning().gemm_splits.load();  // measurement override
   if (v >= 2) {                                // about v segments per tile, all tiles shared
@@ -1545,7 +1980,7 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
     for (int64_t t = 0; t < tiles - dp; ++t)
       maxseg = std::max(maxseg, host_sk_owner(t * pl.U + pl.U - 1, TU, sk) -
                                     host_sk_owner(t * pl.U, TU, sk) + 1);
-    const size_t ws = maxseg > 1 ? (size_t)(tiles - dp) * maxseg * RBM * RBN * 2 : 0;
+    const size_t ws = maxseg > 1 ? (size_t)(tiles - dp) * maxseg * tile_elems * 2 : 0;
     if (ws <= ws_bytes) {
       pl.dp = (int)dp;
       pl.sk = (int)sk;
@@ -1558,12 +1993,46 @@ RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) 
   return pl;
 }
 
+RingPlan ring_plan(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  const int64_t tiles = ((N + RBN - 1) / RBN) * ((M + RBM - 1) / RBM);
+  const int KS = wbits == 4 ? Ring<4>::KS : wbits == 8 ? Ring<8>::KS : Ring<16>::KS;
+  return split_plan(tiles, (int)((K / RBK + KS - 1) / KS), RBM * RBN, ws_bytes);
+}
+
+// The specialised-wave kernel: INT4, whole 128-column tiles, whole super-steps.
+bool gemm_spec_ok(int64_t M, int64_t N, int64_t K, int wbits) {
+  return wbits == 4 && gemm_ring_ok(M, N, K, wbits) && N % SBN == 0 &&
+         K % (RBK * kSpecKS) == 0;
+}
+
+RingPlan spec_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
+  const int64_t tiles = (N / SBN) * ((M + SBM - 1) / SBM);
+  return split_plan(tiles, (int)(K / (RBK * kSpecKS)), SBM * SBN, ws_bytes);
+}
+
+// Kernel for M >= 256: the ring kernel, or the specialised-wave kernel where
+// it applies when the gemm_kernel knob is 2.  Measured on config 3 (M = 512,
+// INT4) the two take the same time (3a 136-141 against 135-141 us, 3b
+// 130-136 against 130-132 us): the 256 x 128 tile the register budget of
+// two waves per SIMD allows copies twice the X bytes per FLOP of the ring
+// kernel's 256 x 256 tile, and the X copies (16 KB per K step per CU) then
+// bound its K step as the single-wave issue bounds the ring kernel's.
+bool use_spec(int64_t M, int64_t N, int64_t K, int wbits) {
+  return tuning().gemm_kernel.load() == 2 && gemm_spec_ok(M, N, K, wbits);
+}
+
 int gemm_splits(int64_t M, int64_t N, int64_t K, int wbits, size_t ws_bytes) {
+  if (use_spec(M, N, K, wbits)) return spec_plan(M, N, K, ws_bytes).maxseg;
   return gemm_ring_ok(M, N, K, wbits) ? ring_plan(M, N, K, wbits, ws_bytes).maxseg : 1;
 }
 
+// Workspace for the larger of the two kernels' plans, so that a workspace
+// sized once serves either choice of the gemm_kernel knob.
 size_t gemm_ws_bytes(int64_t M, int64_t N, int64_t K, int wbits) {
-  return gemm_ring_ok(M, N, K, wbits) ? ring_plan(M, N, K, wbits, (size_t)-1).ws : 0;
+  if (!gemm_ring_ok(M, N, K, wbits)) return 0;
+  size_t ws = ring_plan(M, N, K, wbits, (size_t)-1).ws;
+  if (gemm_spec_ok(M, N, K, wbits)) ws = std::max(ws, spec_plan(M, N, K, (size_t)-1).ws);
+  return ws;
 }
 
 int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int64_t M, int64_t N,
@@ -1572,6 +2041,22 @@ int gemm_mfma_launch(const void* x, const void* w, const void* sz, void* y, int6
   const auto* wp = static_cast<const uint8_t*>(w);
   const auto* sp = static_cast<const uint32_t*>(sz);
   auto* yp = static_cast<uint16_t*>(y);
+  if (use_spec(M, N, K, wbits)) {
+    const RingPlan pl = spec_plan(M, N, K, ws ? ws_bytes : 0);
+    uint16_t* part = pl.ws ? static_cast<uint16_t*>(ws) : nullptr;
+    hipLaunchKernelGGL(gemm_spec_kernel, dim3((unsigned)(pl.dp + pl.sk)), dim3(kSpecThreads), 0,
+                       st, xp, wp, sp, yp, part, (int)M, (int)N, (int)K, pl.dp, pl.sk, pl.U,
+                       pl.maxseg);
+    R4Q_TRY(launch_status("gemm_spec"));
+    if (pl.ws) {
+      const int64_t tiles = (N / SBN) * ((M + SBM - 1) / SBM);
+      const unsigned rb = (unsigned)((tiles - pl.dp) * (kSpecRedThreadsPerTile / 256));
+      hipLaunchKernelGGL(gemm_spec_reduce_kernel, dim3(rb), dim3(256), 0, st, part, yp, (int)M,
+                         (int)N, pl.dp, pl.sk, pl.U, pl.maxseg);
+      R4Q_TRY(launch_status("gemm_spec_reduce"));
+    }
+    return R4Q_OK;
+  }
   if (gemm_ring_ok(M, N, K, wbits)) {
     const RingPlan pl = ring_plan(M, N, K, wbits, ws ? ws_bytes : 0);
     uint16_t* part = pl.ws ? static_cast<uint16_t*>(ws) : nullptr;

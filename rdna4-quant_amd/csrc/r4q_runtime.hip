@@ -46,6 +46,7 @@ const Knob kKnobs[] = {
     {"skinny_splits", "R4Q_SKINNY_SPLITS", &Tuning::skinny_splits, 1, 8, false},
     {"gemm_splits", "R4Q_GEMM_SPLITS", &Tuning::gemm_splits, 1, 16, false},
     {"split_reduce", "R4Q_SPLIT_REDUCE", &Tuning::split_reduce, 1, 1, false},
+    {"gemm_kernel", "R4Q_GEMM_KERNEL", &Tuning::gemm_kernel, 1, 2, false},
 };
 
 bool knob_ok(const Knob& k, long x) {

@@ -282,3 +282,75 @@ def test_ring_gemm_forced_split_counts(dev, splits):
         R.tune("gemm_splits", 0)
     assert rel_l2(got, base) <= 1e-3
     assert rel_l2(got, O.gemm(x.numpy(), w.numpy(), sz.numpy(), 4)) <= TOL
+
+
+def _spec(fn):
+    """Runs fn with the specialised-wave GEMM kernel selected."""
+    import r4q_lib as R
+    R.tune("gemm_kernel", 2)
+    try:
+        return fn()
+    finally:
+        R.tune("gemm_kernel", 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 17408, 5120), (512, 5120, 17408), (600, 256, 4096),
+                                   (512, 7168, 5120), (300, 1280, 2048)])
+def test_spec_gemm_vs_oracle_and_ring(dev, M, N, K):
+    """The specialised-wave kernel (INT4, N % 128 == 0, K % 256 == 0): config
+    3 shapes, a ragged M and split-K shapes against the oracle, and against
+    the ring kernel within fp32 / fp16-partial rounding."""
+    g = S.gen(M + 5 * N + K)
+    w, sz = S.int4_weight(N, K, g)
+    x = torch.randn(M, K, generator=g).half()
+    X, Wd, SZ = x.to(dev), w.to(dev), sz.to(dev)
+    ring = int4_hip.dbg_gemm(X, Wd, SZ, M, N, K).float().cpu().numpy()
+    got = _spec(lambda: int4_hip.dbg_gemm(X, Wd, SZ, M, N, K)).float().cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert rel_l2(got, ring) <= 1e-3
+    want = _ref32(x, w, sz, 4) if N * K > 4e7 else O.gemm(x.numpy(), w.numpy(), sz.numpy(), 4)
+    assert rel_l2(got, want) <= TOL
+    for r in (0, M // 2, M - 1):
+        assert rel_l2(got[r], want[r]) <= TOL, r
+
+
+def test_spec_gemm_whole_tiles_bit_identical_to_ring(dev):
+    """With whole tiles only (gemm_splits 1) every output element sees the same
+    MFMA sequence in both kernels: bit-identical results."""
+    import r4q_lib as R
+    M, N, K = 512, 1024, 2048
+    g = S.gen(123)
+    w, sz = S.int4_weight(N, K, g)
+    x = torch.randn(M, K, generator=g).half()
+    X, Wd, SZ = x.to(dev), w.to(dev), sz.to(dev)
+    R.tune("gemm_splits", 1)
+    try:
+        ring = int4_hip.dbg_gemm(X, Wd, SZ, M, N, K).cpu().numpy()
+        got = _spec(lambda: int4_hip.dbg_gemm(X, Wd, SZ, M, N, K)).cpu().numpy()
+    finally:
+        R.tune("gemm_splits", 0)
+    assert np.array_equal(got.view(np.uint16), ring.view(np.uint16))
+
+
+@pytest.mark.parametrize("splits", [0, 3])
+def test_spec_gemm_one_hot_columns_exact(dev, splits):
+    """Row r of x = e_k(r): y[r] is column k(r) of the dequantised weight, bit
+    for bit, through the specialised-wave kernel's B stages -- in the default
+    plan and with every tile shared by about 3 workgroups (fp16 partials of
+    zeros and one exact product, summed by its reduce)."""
+    import r4q_lib as R
+    g = S.gen(211 + splits)
+    M, N, K = 300, 384, 2048
+    w, sz = S.int4_weight(N, K, g)
+    W = O.dequant(w.numpy(), sz.numpy(), 4)
+    ks = [(r * 631 + r // 5) % K for r in range(M)]
+    x = torch.zeros(M, K, dtype=torch.float16)
+    for r, k in enumerate(ks):
+        x[r, k] = 1.0
+    R.tune("gemm_splits", splits)
+    try:
+        y = _spec(lambda: int4_hip.dbg_gemm(x.to(dev), w.to(dev), sz.to(dev), M, N, K)).cpu().numpy()
+    finally:
+        R.tune("gemm_splits", 0)
+    for r, k in enumerate(ks):
+        assert np.array_equal(y[r], W[:, k]), (r, k)
