@@ -2012,11 +2012,12 @@ RingPlan spec_plan(int64_t M, int64_t N, int64_t K, size_t ws_bytes) {
 
 // Kernel for M >= 256: the ring kernel, or the specialised-wave kernel where
 // it applies when the gemm_kernel knob is 2.  Measured on config 3 (M = 512,
-// INT4) the two take the same time (3a 136-141 against 135-141 us, 3b
-// 130-136 against 130-132 us): the 256 x 128 tile the register budget of
-// two waves per SIMD allows copies twice the X bytes per FLOP of the ring
-// kernel's 256 x 256 tile, and the X copies (16 KB per K step per CU) then
-// bound its K step as the single-wave issue bounds the ring kernel's.
+// INT4, five A/B pairs on one box) the latter is the slower of the two (3a
+// 140-146 against 132-137 us, 3b 131-141 against 126-131 us): the 256 x 128
+// tile that the register budget of two waves per SIMD allows copies twice
+// the X bytes per FLOP of the ring kernel's 256 x 256 tile, and the X copies
+// (16 KB per K step per CU) then bound its K step as the single-wave issue
+// bounds the ring kernel's.
 bool use_spec(int64_t M, int64_t N, int64_t K, int wbits) {
   return tuning().gemm_kernel.load() == 2 && gemm_spec_ok(M, N, K, wbits);
 }
