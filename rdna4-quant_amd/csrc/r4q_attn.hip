@@ -576,15 +576,18 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
 
 int attn_num_splits(int64_t cap_len, int64_t B, int64_t Hk) {
   // About 128 positions of the cache capacity per split, at most 32 splits
-  // and at most 512 workgroups (2 per CU at the kernel's register use);
-  // measured on MI355X with cold caches at 2K-32K contexts, batch 1 and 8
-  // (32 splits against 64: 10.5 vs 10.9 us at 8K, 18.3 vs 19.0 us at 32K).
-  // Depends only on the cache capacity, so a captured graph stays valid as
-  // the sequence grows.
+  // and at most 256 workgroups (one per CU); measured on MI355X with cold
+  // caches at 2K-32K contexts (32 splits against 64: 10.5 vs 10.9 us at 8K,
+  // 18.3 vs 19.0 us at 32K) and in the batched decode step at ctx 2048,
+  // where a 512-workgroup cap was slower (ms per step, 256 against 512:
+  // batch 2 3.534 / 3.542, batch 4 3.639 / 3.665, batch 8 3.814 / 3.828,
+  // at ctx 8192 4.373 / 4.411, batch 16 4.639 / 4.665).  Depends only on
+  // the cache capacity, so a captured graph stays valid as the sequence
+  // grows.
   if (const int v = tuning().attn_splits.load()) return v;  // measurement override (r4q_tune)
   int64_t n = (cap_len + 127) / 128;
   if (n > 32) n = 32;
-  const int64_t by_wg = 512 / (B * Hk > 0 ? B * Hk : 1);
+  const int64_t by_wg = 256 / (B * Hk > 0 ? B * Hk : 1);
   if (n > by_wg) n = by_wg;
   return (int)(n < 1 ? 1 : n);
 }
