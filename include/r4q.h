@@ -395,10 +395,13 @@ R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hid
  * the qkv, o and down projections in their own launches, not in the
  * attention prologue / row norm that consume them), "gemm_kernel" (GEMM for
  * M >= 256: 1 = the ring kernel (the default), 2 = the specialised-wave
- * kernel where it applies: INT4, N % 128 == 0, K % 256 == 0).  Initial values come
- * from R4Q_GEMV_LPR, R4Q_GEMV_WGS, R4Q_GEMV_UB, R4Q_ATTN_SPLITS,
- * R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, R4Q_SPLIT_REDUCE, R4Q_GEMM_KERNEL, read
- * once.  Results do
+ * kernel where it applies: INT4, N % 128 == 0, K % 256 == 0), "gemv_skew"
+ * (GEMV on an even grid of more than 256 equal shares: the first half of the
+ * workgroups takes value - 1 steps more and the second half value - 1 fewer;
+ * 1 = equal shares; default 2 when each share has at least 4 steps).
+ * Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS, R4Q_GEMV_UB,
+ * R4Q_ATTN_SPLITS, R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, R4Q_SPLIT_REDUCE,
+ * R4Q_GEMM_KERNEL, R4Q_GEMV_SKEW, read once.  Results do
  * not depend on these choices beyond fp32 summation order (split counts) --
  * they exist for sweeps and tests.  Captured decode graphs are keyed by the
  * values in force. */

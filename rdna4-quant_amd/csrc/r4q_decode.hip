@@ -594,7 +594,7 @@ std::vector<uint8_t> graph_key(const r4q_ctx* ctx, int kind, const r4q_model* m,
   const Tuning& tu = tuning();
   const int knobs[] = {tu.gemv_lpr.load(),      tu.gemv_wgs.load(),    tu.gemv_ub.load(),
                        tu.attn_splits.load(),   tu.skinny_splits.load(), tu.gemm_splits.load(),
-                       tu.split_reduce.load(),  tu.gemm_kernel.load()};
+                       tu.split_reduce.load(),  tu.gemm_kernel.load(), tu.gemv_skew.load()};
   std::vector<uint8_t> k(sizeof(r4q_model) + sizeof(r4q_layer) * m->n_layers + 16 +
                          sizeof(extra) + sizeof(epoch) + sizeof(SampleCfg) + sizeof(knobs));
   uint8_t* p = k.data();

@@ -281,6 +281,9 @@ struct GemvNorm {
   // [split, I) (indexed by element) and the split point (a multiple of 32)
   float* h;
   int split;
+  // linear map only: the first half of the workgroups take `skew` steps
+  // more than the second half, which take `skew` fewer
+  int skew = 0;
 };
 
 // Inputs of the fused-norm staging, requested before the first weight steps:
@@ -487,6 +490,7 @@ struct GemvTile {
 template <int RPS, int EPI>
 struct RowMap {
   int g, G, nsteps;  // linear
+  int skew = 0, per = 0;  // linear, skewed: per = nsteps / G exactly
   int I, nunits;     // SiLU: I = N / 2; nunits = I / 32 (unit) or F (split)
   int npairs;        // split: pair steps after the units
   float* h;          // split: fp32 products, indexed by element
@@ -496,6 +500,7 @@ struct RowMap {
     if constexpr (EPI == kEpiSiluUnit) return g < nunits ? ((nunits - g + G - 1) / G) * SPU : 0;
     else if constexpr (EPI == kEpiSiluPair)
       return nunit_steps() + (g < npairs ? ((npairs - g + G - 1) / G) * 2 : 0);
+    else if (skew > 0) return g < G / 2 ? per + skew : per - skew;
     else return g < nsteps ? (nsteps - g + G - 1) / G : 0;
   }
   __device__ int row0(int k) const {
@@ -509,6 +514,7 @@ struct RowMap {
       const int p0 = 32 * nunits + RPS * (g + G * (kk >> 1));
       return (kk & 1) ? I + p0 : p0;
     } else {
+      if (skew > 0 && k >= per - skew) return ((per - skew) * G + (k - (per - skew)) * (G / 2) + g) * RPS;
       return (g + G * k) * RPS;
     }
   }
@@ -665,6 +671,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   map.nunits = EPI == kEpiSiluPair ? nm.split / 32 : N / 64;
   map.npairs = (N / 2 - nm.split) / RPS;
   map.h = nm.h;
+  if constexpr (EPI == kEpiRows) {
+    map.skew = nm.skew;
+    map.per = map.nsteps / map.G;
+  }
   const int nloc = map.nlocal();
 
   NormIn nin;
@@ -809,8 +819,20 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
                                                   2 * (((N / 2 - norm->split) / rps + grid - 1) / grid)
                                             : per;
   const int ub = (int)std::max<int64_t>(1, std::min<int64_t>(ub_o ? ub_o : 1, spw));
+  // Two workgroups per CU: the CU's second workgroup (the second half of
+  // the grid, dispatched once every CU holds one) stages its activation
+  // beside the first and finishes its equal share ~1.4 us later (in-kernel
+  // stamps, 512-workgroup down projection: first half's exits median 9.3-9.4
+  // us, second half's 10.8 us).  So an even grid of equal shares gives the
+  // first half one step more and the second half one step less (40-layer
+  // step 2.637 -> 2.623 ms; two steps: 2.632 ms).  gemv_skew overrides the
+  // difference: value - 1 steps (1 = equal shares).
+  int skew = per >= 4 ? 1 : 0;
+  if (const int v = tuning().gemv_skew.load()) skew = v - 1;
+  if (!(epi == kEpiRows && grid > 256 && grid % 2 == 0 && grid * per == nsteps && skew < per))
+    skew = 0;
   // the staging area also holds one partial per (step, wave) of the workgroup
-  const size_t lds_all = lds > (size_t)per * 16 ? lds : (size_t)per * 16;
+  const size_t lds_all = lds > (size_t)(per + skew) * 16 ? lds : (size_t)(per + skew) * 16;
   R4Q_REQUIRE(lds_all <= 64 * 1024, "gemv: N=%lld too large for one launch", (long long)N);
   const dim3 gd((unsigned)grid), bd(256);
   const auto* xp = static_cast<const uint16_t*>(x);
@@ -822,7 +844,8 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
     R4Q_REQUIRE(norm && norm->split >= 0 && norm->split <= K && norm->split % 32 == 0 &&
                     (norm->h || norm->split == K) && (x || norm->split == 0),
                 "gemv: bad FWHT staging split");
-  const GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
+  GemvNorm nm = norm ? *norm : GemvNorm{nullptr, nullptr, nullptr, 0.f};
+  nm.skew = skew;
 #define R4Q_GEMV_K(L, U, XM, EPI)                                                             \
   hipLaunchKernelGGL((gemv_kernel<WBITS, L, kCpl, U, XM, EPI>), gd, bd, lds_all, st, xp, wp, sp, \
                      yp, (int)N, (int)K, nm)

@@ -33,13 +33,16 @@ int launch_status(const char* what);
 //   gemm_kernel   R4Q_GEMM_KERNEL   GEMM for M >= 256: 1 the ring kernel (the default), 2 the
 //                                   specialised-wave kernel where it applies (INT4, N % 128 == 0,
 //                                   K % 256 == 0)
+//   gemv_skew     R4Q_GEMV_SKEW     GEMV on an even grid of more than 256 equal shares: the
+//                                   first half takes value - 1 steps more, the second half
+//                                   value - 1 fewer (1 = equal shares)
 //   split_reduce  R4Q_SPLIT_REDUCE  1: batched decode steps reduce the split-K partials of the
 //                                   qkv, o and down projections in their own launches instead
 //                                   of in the consumer (attention prologue, row norm)
 struct Tuning {
   std::atomic<int> gemv_lpr{0}, gemv_wgs{0}, gemv_ub{0};
   std::atomic<int> attn_splits{0}, skinny_splits{0}, gemm_splits{0};
-  std::atomic<int> split_reduce{0}, gemm_kernel{0};
+  std::atomic<int> split_reduce{0}, gemm_kernel{0}, gemv_skew{0};
 };
 Tuning& tuning();
 

@@ -47,6 +47,7 @@ const Knob kKnobs[] = {
     {"gemm_splits", "R4Q_GEMM_SPLITS", &Tuning::gemm_splits, 1, 16, false},
     {"split_reduce", "R4Q_SPLIT_REDUCE", &Tuning::split_reduce, 1, 1, false},
     {"gemm_kernel", "R4Q_GEMM_KERNEL", &Tuning::gemm_kernel, 1, 2, false},
+    {"gemv_skew", "R4Q_GEMV_SKEW", &Tuning::gemv_skew, 1, 8, false},
 };
 
 bool knob_ok(const Knob& k, long x) {

@@ -37,6 +37,25 @@ def test_gemv_qwen3_shapes(dev, bits, N, K):
     assert rel_l2(got, want) <= TOL
 
 
+def test_gemv_skewed_shares_bit_identical(dev):
+    """The INT4 down projection runs 512 workgroups of 5 steps; by default the
+    first half of the grid takes one step more and the second half one fewer.
+    Every row is still reduced whole by one workgroup, so equal shares and
+    skews of 1-3 steps give the same bits, and the default matches the
+    oracle."""
+    import r4q_lib as R
+    got = {}
+    try:
+        for v in (0, 1, 3, 4):
+            R.tune("gemv_skew", v)
+            got[v], want, _ = _run(dev, 4, 5120, 17408, seed=41)
+    finally:
+        R.tune("gemv_skew", 0)
+    for v in (0, 3, 4):
+        assert np.array_equal(got[v].view(np.uint16), got[1].view(np.uint16)), v
+    assert rel_l2(got[0], want) <= TOL
+
+
 @pytest.mark.parametrize("bits", [4, 8, 16])
 @pytest.mark.parametrize("N,K", [(1, 32), (3, 64), (7, 160), (100, 256), (33, 1024), (65, 1536),
                                  (129, 4096), (5, 10240), (2, 2176 * 8)])
