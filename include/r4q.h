@@ -398,7 +398,8 @@ R4Q_API int r4q_decode_profile(r4q_ctx* ctx, const r4q_model* m, const void* hid
  * kernel where it applies: INT4, N % 128 == 0, K % 256 == 0), "gemv_skew"
  * (GEMV on an even grid of more than 256 equal shares: the first half of the
  * workgroups takes value - 1 steps more and the second half value - 1 fewer;
- * 1 = equal shares; default 2 when each share has at least 4 steps).
+ * 1 = equal shares; default 2 on a 512-workgroup grid of at least 4 steps
+ * each).
  * Initial values come from R4Q_GEMV_LPR, R4Q_GEMV_WGS, R4Q_GEMV_UB,
  * R4Q_ATTN_SPLITS, R4Q_SKINNY_SPLITS, R4Q_GEMM_SPLITS, R4Q_SPLIT_REDUCE,
  * R4Q_GEMM_KERNEL, R4Q_GEMV_SKEW, read once.  Results do

@@ -823,11 +823,12 @@ int launch_gemv_fmt(const void* x, const void* w, const void* sz, void* y, int64
   // the grid, dispatched once every CU holds one) stages its activation
   // beside the first and finishes its equal share ~1.4 us later (in-kernel
   // stamps, 512-workgroup down projection: first half's exits median 9.3-9.4
-  // us, second half's 10.8 us).  So an even grid of equal shares gives the
-  // first half one step more and the second half one step less (40-layer
+  // us, second half's 10.8 us).  So a grid of two equal shares per CU gives
+  // the first half one step more and the second half one step less (40-layer
   // step 2.637 -> 2.623 ms; two steps: 2.632 ms).  gemv_skew overrides the
-  // difference: value - 1 steps (1 = equal shares).
-  int skew = per >= 4 ? 1 : 0;
+  // difference: value - 1 steps (1 = equal shares) on any even grid of
+  // more than 256 equal shares.
+  int skew = per >= 4 && grid == 2 * 256 ? 1 : 0;
   if (const int v = tuning().gemv_skew.load()) skew = v - 1;
   if (!(epi == kEpiRows && grid > 256 && grid % 2 == 0 && grid * per == nsteps && skew < per))
     skew = 0;
