@@ -162,3 +162,29 @@ def test_model_cache_key_follows_storage_swaps():
     assert kn == int4_hip._key_of([[None, ws[0]]])
     ws[0].set_(torch.zeros(8, dtype=torch.uint8))
     assert int4_hip._key_of([[None, ws[0]]]) != kn
+
+
+# (name, lowest, highest, power of two only) as include/r4q.h documents r4q_tune
+KNOBS = [("gemv_lpr", 16, 256, True), ("gemv_wgs", 1, 65536, False), ("gemv_ub", 1, 2, False),
+         ("attn_splits", 1, 128, False), ("skinny_splits", 1, 8, False),
+         ("gemm_splits", 1, 16, False), ("split_reduce", 1, 1, False),
+         ("gemm_kernel", 1, 2, False), ("gemv_skew", 1, 8, False)]
+
+
+def test_tune_accepts_documented_knobs_and_rejects_the_rest():
+    L = R.lib()
+    try:
+        for name, lo, hi, pow2 in KNOBS:
+            n = name.encode()
+            assert L.r4q_tune(n, lo) == R.R4Q_OK, name
+            assert L.r4q_tune(n, hi) == R.R4Q_OK, name
+            _einval(L.r4q_tune(n, lo - 1 if lo > 1 else -1))
+            _einval(L.r4q_tune(n, hi + 1))
+            if pow2:
+                _einval(L.r4q_tune(n, lo + 1))
+            assert L.r4q_tune(n, 0) == R.R4Q_OK, name  # back to the built-in choice
+        _einval(L.r4q_tune(b"no_such_knob", 1))
+        _einval(L.r4q_tune(None, 1))
+    finally:
+        for name, *_ in KNOBS:
+            L.r4q_tune(name.encode(), 0)
