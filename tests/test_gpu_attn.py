@@ -65,6 +65,14 @@ def test_flash_decode_batch8_no_rotation(dev, ctx):
     _case(dev, ctx, 8, 40, 8, 700, 1024, scaled=False, fwht=False, seed=8)
 
 
+@pytest.mark.parametrize("B", [2, 4, 16])
+def test_flash_decode_batches_at_the_workgroup_cap(dev, ctx, B):
+    """ctx 2048 at the default split count, which keeps B x 8 KV heads x
+    splits within one workgroup per CU: 16, 8 and 2 splits for batches 2, 4
+    and 16 (XCD-grouped grids, merge rounds of 16 and 8)."""
+    _case(dev, ctx, B, 40, 8, 2048, 2048 + 40, scaled=True, fwht=True, seed=100 + B)
+
+
 @pytest.mark.parametrize("L", [257, 8192])
 def test_flash_decode_forced_split_counts(dev, ctx, L):
     """Split counts from 1 to 128 back to back on one context: more than one
