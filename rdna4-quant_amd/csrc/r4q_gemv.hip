@@ -282,7 +282,7 @@ struct GemvNorm {
   float* h;
   int split;
   // linear map only: the first half of the workgroups take `skew` steps
-  // more than the second half, which take `skew` fewer
+  // more than an equal share, the second half `skew` fewer
   int skew = 0;
 };
 
@@ -514,7 +514,8 @@ struct RowMap {
       const int p0 = 32 * nunits + RPS * (g + G * (kk >> 1));
       return (kk & 1) ? I + p0 : p0;
     } else {
-      if (skew > 0 && k >= per - skew) return ((per - skew) * G + (k - (per - skew)) * (G / 2) + g) * RPS;
+      if (skew > 0 && k >= per - skew)  // past the common steps: first half only
+        return ((per - skew) * G + (k - (per - skew)) * (G / 2) + g) * RPS;
       return (g + G * k) * RPS;
     }
   }
